@@ -1,0 +1,43 @@
+"""MI355X (gfx950) causal sliding-window attention backend for hackable-lm.
+
+Public surface:
+  attention(q, k, v, window_size=None)        differentiable (B,T,H,D) bf16 attention
+  scaled_dot_product_attention(...)           the reference's dispatch signature, backend="hip"
+  AttentionCore                               model.py's attention module with fwd_hip
+  ATTENTION_BACKENDS, layer_attention_window  config.py's names and layer pattern
+  hip_attention_available, resolve_attention_backend
+The kernels live in libhlm_attn.so (built by hlm_attn.build), reached through
+the C ABI in include/hlm_attn.h.
+"""
+from .config import (
+    ATTENTION_BACKENDS,
+    HIP_BACKEND,
+    attention_window_size,
+    layer_attention_window,
+    normalize_attention_backend,
+    normalize_attention_full_every,
+    normalize_attention_window,
+)
+from .kernels import (
+    attention,
+    hip_attention_available,
+    resolve_attention_backend,
+    scaled_dot_product_attention,
+)
+from .model import AttentionConfig, AttentionCore
+
+__all__ = [
+    "ATTENTION_BACKENDS",
+    "HIP_BACKEND",
+    "AttentionConfig",
+    "AttentionCore",
+    "attention",
+    "attention_window_size",
+    "hip_attention_available",
+    "layer_attention_window",
+    "normalize_attention_backend",
+    "normalize_attention_full_every",
+    "normalize_attention_window",
+    "resolve_attention_backend",
+    "scaled_dot_product_attention",
+]

@@ -1,0 +1,70 @@
+"""ctypes binding of libhlm_attn.so (the C ABI declared in include/hlm_attn.h).
+
+No torch types cross this boundary: tensors are passed as device pointers plus
+int64 strides, the stream as a raw hipStream_t handle.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
+ABI_VERSION = 1
+
+# Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_S = ctypes.POINTER(ctypes.c_int64)
+SIGNATURES = {
+    "hlm_attn_abi_version": (_I, []),
+    "hlm_attn_last_error": (ctypes.c_char_p, []),
+    "hlm_attn_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _I, _F, _P]),
+    "hlm_attn_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class HipAttentionUnavailable(RuntimeError):
+    """The compiled HIP attention library is missing or unusable."""
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Loads (once) and returns the library; raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    target = Path(path) if path is not None else LIB_PATH
+    if not target.exists():
+        raise HipAttentionUnavailable(
+            f"{target} is missing: build it with `python -m hlm_attn.build` "
+            "(hipcc --offload-arch=gfx950) before using attention_backend='hip'"
+        )
+    lib = ctypes.CDLL(str(target))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.hlm_attn_abi_version() != ABI_VERSION:
+        raise HipAttentionUnavailable(
+            f"{target} has ABI {lib.hlm_attn_abi_version()}, this binding expects {ABI_VERSION}"
+        )
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def strides3(t) -> ctypes.Array:
+    """(batch, time, head) strides of a (B, T, H, D) tensor as an int64[3]."""
+    s = t.stride()
+    return (ctypes.c_int64 * 3)(s[0], s[1], s[2])
+
+
+def check(rc: int, lib: ctypes.CDLL) -> None:
+    if rc != 0:
+        msg = lib.hlm_attn_last_error().decode(errors="replace")
+        raise RuntimeError(f"hip attention failed (code {rc}): {msg}")

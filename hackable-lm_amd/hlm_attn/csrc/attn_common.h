@@ -1,0 +1,162 @@
+// Shared device helpers for the gfx950 causal sliding-window attention kernels.
+//
+// Conventions used by every kernel in this library
+// -------------------------------------------------
+// * Tensors q, k, v, o, dO, dq, dk, dv are bf16 in (B, T, H, D) order with unit
+//   stride along D and arbitrary (16-byte aligned) strides along B, T, H.
+// * lse and delta are fp32 (B, H, T), contiguous.  lse is the natural-log
+//   log-sum-exp of the scaled, masked scores of each query row.
+// * Query i sees keys j with  i - W < j <= i  (W = window, W >= T means plain
+//   causal), the rule of hackable-lm's model.py:143-153.
+// * All contractions use v_mfma_f32_32x32x16_bf16.  For one wave (64 lanes):
+//     A operand (32 x 16):  lane l holds A[l % 32][8 * (l / 32) + e], e = 0..7
+//     B operand (16 x 32):  lane l holds B[8 * (l / 32) + e][l % 32]
+//     C/D (32 x 32, fp32):  lane l holds C[8 * i + 4 * (l / 32) + j][l % 32]
+//                           in acc[4 * i + j], i, j = 0..3
+//   (checked against a host matmul on the MI355X before these kernels were
+//   written).
+// * "key order" of a 16-wide contraction step: the accumulator values
+//   acc[8 t .. 8 t + 7] of a 32-row block, taken as the 8 B-operand values of
+//   contraction step t, cover the rows sigma(8 * (l / 32) + e) of the 16-row
+//   group 16 t .. 16 t + 15 with sigma = [0,1,2,3,8,9,10,11,4,5,6,7,12,13,14,15].
+//   lds_operand_tr() reads the other operand of that contraction in the same
+//   order, so the pair contracts over the right rows without any shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hlm {
+
+typedef __bf16 bf16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kThreads = 256;  // 4 waves of 64
+
+struct FwdArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  bf16* o;
+  float* lse;
+  int64_t sq[3], sk[3], sv[3], so[3];  // (batch, time, head) strides in elements
+  int B, T, H, Hkv, W;                 // 1 <= W <= T
+  float scale_log2;                    // softmax scale * log2(e)
+};
+
+struct BwdArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const bf16* o;
+  const bf16* dout;
+  const float* lse;
+  bf16* dq;
+  bf16* dk;
+  bf16* dv;
+  float* delta;  // (B, H, T) workspace: rowsum(dO * O), written by the dq kernel
+  int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3];
+  int B, T, H, Hkv, W;
+  float scale;       // softmax scale
+  float scale_log2;  // scale * log2(e)
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
+  return z;
+}
+
+// Maps a linear workgroup id onto a tile index so that the workgroups that the
+// hardware places on one XCD (ids congruent mod 8) get a contiguous range of
+// tiles.  Neighbouring tiles of one (batch, head) then share that XCD's L2.
+__device__ __forceinline__ int xcd_swizzle(int id, int n) {
+  const int xcd = id & 7, slot = id >> 3;
+  const int per = n >> 3, extra = n & 7;
+  return xcd * per + min(xcd, extra) + slot;
+}
+
+// A/B operand whose 8 contraction values sit contiguously in one LDS row:
+// lane l reads x[(l % 32) * stride + 8 * (l / 32) .. + 7].
+__device__ __forceinline__ bf16x8 lds_operand(const bf16* x, int stride, int lane) {
+  return *reinterpret_cast<const bf16x8*>(x + (lane & 31) * stride + 8 * (lane >> 5));
+}
+
+// A/B operand that contracts over the ROWS of a row-major LDS tile x (16 rows
+// of one contraction step, 32 columns of the output): lane l receives
+// x[sigma(8 * (l / 32) + e) * stride + (l % 32)], e = 0..7, via two
+// ds_read_b64_tr_b16.  Within a 16-lane group, lanes 4r..4r+3 supply the four
+// 8-byte pieces of row r of a 4 x 16 block and lane i receives column i.
+__device__ __forceinline__ bf16x8 lds_operand_tr(const bf16* x, int stride, int lane) {
+  const int g = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
+  const bf16* p0 = x + (4 * (g >> 1) + r) * stride + 16 * (g & 1) + 4 * c;
+  const bf16* p1 = p0 + 8 * stride;
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
+  bf16x8 out;
+  const bf16x4 lo_b = __builtin_bit_cast(bf16x4, lo);
+  const bf16x4 hi_b = __builtin_bit_cast(bf16x4, hi);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    out[e] = lo_b[e];
+    out[4 + e] = hi_b[e];
+  }
+  return out;
+}
+
+// Global -> register -> LDS copy of a ROWS x D bf16 tile (row-major in both
+// places, LDS row stride D + 8 elements).  Rows at or beyond `nrows` read as 0.
+// Each thread moves 16-byte chunks; consecutive threads take consecutive
+// chunks of a row, so every global access is a coalesced 128-bit load.
+template <int ROWS, int D>
+struct RowTile {
+  static constexpr int kChunksPerRow = D / 8;
+  static constexpr int kChunks = ROWS * kChunksPerRow;
+  static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+  static constexpr bool kExact = (kChunks % kThreads) == 0;
+  uint4 r[kPer];
+
+  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int r0, int nrows,
+                                       int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * kThreads;
+      const int row = c / kChunksPerRow, col = (c % kChunksPerRow) * 8;
+      r[i] = make_uint4(0u, 0u, 0u, 0u);
+      if ((kExact || c < kChunks) && r0 + row < nrows)
+        r[i] = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + row) * row_stride + col);
+    }
+  }
+
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * kThreads;
+      const int row = c / kChunksPerRow, col = (c % kChunksPerRow) * 8;
+      if (kExact || c < kChunks) *reinterpret_cast<uint4*>(lds + row * (D + 8) + col) = r[i];
+    }
+  }
+};
+
+}  // namespace hlm

@@ -1,0 +1,152 @@
+// extern "C" entry points of libhlm_attn.so (declared in include/hlm_attn.h):
+// argument validation, mask normalisation and kernel dispatch by head dim.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "attn_common.h"
+#include "../../../include/hlm_attn.h"
+
+namespace hlm {
+template <int D>
+hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
+template <int D>
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
+}  // namespace hlm
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_tensor(const char* name, const void* p, const int64_t* s) {
+  if (p == nullptr) return fail(HLM_ATTN_EINVAL, "%s is a null pointer", name);
+  if (!aligned16(p)) return fail(HLM_ATTN_EINVAL, "%s is not 16-byte aligned", name);
+  if (s == nullptr) return fail(HLM_ATTN_EINVAL, "%s strides are a null pointer", name);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || s[i] % 8 != 0)
+      return fail(HLM_ATTN_EINVAL, "%s stride[%d] = %lld must be a non-negative multiple of 8 elements",
+                  name, i, (long long)s[i]);
+  return HLM_ATTN_OK;
+}
+
+int check_dims(int B, int T, int H, int Hkv, int D, float scale) {
+  if (B < 0 || T < 0 || H <= 0 || Hkv <= 0)
+    return fail(HLM_ATTN_EINVAL, "bad shape B=%d T=%d H=%d Hkv=%d", B, T, H, Hkv);
+  if (H % Hkv != 0) return fail(HLM_ATTN_EINVAL, "H=%d is not a multiple of Hkv=%d", H, Hkv);
+  if (D != 64 && D != 128) return fail(HLM_ATTN_EUNSUPPORTED, "head_dim %d is not supported (64 or 128)", D);
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(HLM_ATTN_EINVAL, "scale must be positive and finite");
+  const int64_t tiles = (int64_t)((T + 127) / 128) * H * B;
+  if (tiles >= (int64_t)1 << 31) return fail(HLM_ATTN_EUNSUPPORTED, "problem too large for one launch");
+  return HLM_ATTN_OK;
+}
+
+int effective_window(int window, int T) { return (window <= 0 || window >= T) ? T : window; }
+
+void copy3(int64_t dst[3], const int64_t* src) {
+  for (int i = 0; i < 3; ++i) dst[i] = src[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+int hlm_attn_abi_version(void) { return 1; }
+
+const char* hlm_attn_last_error(void) { return g_last_error; }
+
+int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int T, int H,
+                 int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides, int window, float scale,
+                 void* stream) {
+  g_last_error[0] = '\0';
+  int rc = check_dims(B, T, H, Hkv, D, scale);
+  if (rc) return rc;
+  if (B == 0 || T == 0) return HLM_ATTN_OK;
+  if ((rc = check_tensor("q", q, q_strides)) || (rc = check_tensor("k", k, k_strides)) ||
+      (rc = check_tensor("v", v, v_strides)) || (rc = check_tensor("o", o, o_strides)))
+    return rc;
+  if (lse == nullptr) return fail(HLM_ATTN_EINVAL, "lse is a null pointer");
+  hlm::FwdArgs a;
+  a.q = static_cast<const hlm::bf16*>(q);
+  a.k = static_cast<const hlm::bf16*>(k);
+  a.v = static_cast<const hlm::bf16*>(v);
+  a.o = static_cast<hlm::bf16*>(o);
+  a.lse = lse;
+  copy3(a.sq, q_strides);
+  copy3(a.sk, k_strides);
+  copy3(a.sv, v_strides);
+  copy3(a.so, o_strides);
+  a.B = B;
+  a.T = T;
+  a.H = H;
+  a.Hkv = Hkv;
+  a.W = effective_window(window, T);
+  a.scale_log2 = scale * hlm::kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t err = D == 64 ? hlm::launch_fwd<64>(a, s) : hlm::launch_fwd<128>(a, s);
+  if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
+  return HLM_ATTN_OK;
+}
+
+int hlm_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H,
+                 int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
+                 const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                 int window, float scale, void* stream) {
+  g_last_error[0] = '\0';
+  int rc = check_dims(B, T, H, Hkv, D, scale);
+  if (rc) return rc;
+  if (B == 0 || T == 0) return HLM_ATTN_OK;
+  if ((rc = check_tensor("q", q, q_strides)) || (rc = check_tensor("k", k, k_strides)) ||
+      (rc = check_tensor("v", v, v_strides)) || (rc = check_tensor("o", o, o_strides)) ||
+      (rc = check_tensor("dout", dout, do_strides)) || (rc = check_tensor("dq", dq, dq_strides)) ||
+      (rc = check_tensor("dk", dk, dk_strides)) || (rc = check_tensor("dv", dv, dv_strides)))
+    return rc;
+  if (lse == nullptr) return fail(HLM_ATTN_EINVAL, "lse is a null pointer");
+  if (delta_ws == nullptr) return fail(HLM_ATTN_EINVAL, "delta_ws is a null pointer");
+  hlm::BwdArgs a;
+  a.q = static_cast<const hlm::bf16*>(q);
+  a.k = static_cast<const hlm::bf16*>(k);
+  a.v = static_cast<const hlm::bf16*>(v);
+  a.o = static_cast<const hlm::bf16*>(o);
+  a.dout = static_cast<const hlm::bf16*>(dout);
+  a.lse = lse;
+  a.dq = static_cast<hlm::bf16*>(dq);
+  a.dk = static_cast<hlm::bf16*>(dk);
+  a.dv = static_cast<hlm::bf16*>(dv);
+  a.delta = delta_ws;
+  copy3(a.sq, q_strides);
+  copy3(a.sk, k_strides);
+  copy3(a.sv, v_strides);
+  copy3(a.so, o_strides);
+  copy3(a.sdo, do_strides);
+  copy3(a.sdq, dq_strides);
+  copy3(a.sdk, dk_strides);
+  copy3(a.sdv, dv_strides);
+  a.B = B;
+  a.T = T;
+  a.H = H;
+  a.Hkv = Hkv;
+  a.W = effective_window(window, T);
+  a.scale = scale;
+  a.scale_log2 = scale * hlm::kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t err = D == 64 ? hlm::launch_bwd<64>(a, s) : hlm::launch_bwd<128>(a, s);
+  if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
+  return HLM_ATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+"""torch custom ops over the C ABI: hackable_lm::hip_attn_fwd / hip_attn_bwd.
+
+They are registered the way the reference registers its Triton ops
+(torch.library.custom_op + register_fake + register_autograd,
+/root/reference/kernels.py:320,388,505 and :738-740), so a model that runs
+under torch.compile(fullgraph=True) and CUDA-graph capture
+(/root/reference/kernels.py:126-143) can trace and capture them: the fake
+implementations only describe shapes, and the real ones allocate through
+torch's caching allocator, launch on torch's current stream and never
+synchronise.  There is no CPU implementation: on a tensor that is not on a
+ROCm device, or without libhlm_attn.so, the ops raise.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Returns t if its layout fits the kernels (unit D stride, 16-byte aligned
+    rows), else a contiguous copy."""
+    s = t.stride()
+    ok = (
+        s[3] == 1
+        and all(x >= 0 and x % 8 == 0 for x in s[:3])
+        and t.data_ptr() % 16 == 0
+    )
+    return t if ok else t.contiguous()
+
+
+def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    if q.device.type != "cuda":
+        raise RuntimeError(f"hip attention runs on ROCm devices only, got a tensor on {q.device}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != _BF16:
+            raise RuntimeError(f"hip attention expects bfloat16 {name}, got {t.dtype}")
+        if t.dim() != 4:
+            raise RuntimeError(f"hip attention expects {name} shaped (B, T, H, D), got {tuple(t.shape)}")
+        if t.device != q.device:
+            raise RuntimeError("q, k and v must be on the same device")
+    if k.shape != v.shape:
+        raise RuntimeError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must have the same shape")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise RuntimeError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree on B, T or D")
+    if q.shape[2] % k.shape[2] != 0:
+        raise RuntimeError(f"query heads {q.shape[2]} are not a multiple of kv heads {k.shape[2]}")
+
+
+def _stream_handle(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+@torch.library.custom_op("hackable_lm::hip_attn_fwd", mutates_args=())
+def hip_attn_fwd(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    _check_inputs(q, k, v)
+    lib = _lib.load()
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    B, T, H, D = q.shape
+    o = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.hlm_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            B, T, H, k.shape[2], D,
+            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o),
+            int(window), float(scale), _stream_handle(q.device),
+        )
+    _lib.check(rc, lib)
+    return o, lse
+
+
+@hip_attn_fwd.register_fake
+def _(q, k, v, window, scale):
+    B, T, H, D = q.shape
+    return q.new_empty((B, T, H, D), dtype=_BF16), q.new_empty((B, H, T), dtype=torch.float32)
+
+
+@torch.library.custom_op("hackable_lm::hip_attn_bwd", mutates_args=())
+def hip_attn_bwd(
+    dout: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    window: int,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    _check_inputs(q, k, v)
+    lib = _lib.load()
+    if dout.shape != q.shape or o.shape != q.shape:
+        raise RuntimeError("dout and o must have the shape of q")
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    o = _kernel_ready(o)
+    dout = _kernel_ready(dout.to(_BF16))
+    lse = lse.contiguous()
+    B, T, H, D = q.shape
+    Hkv = k.shape[2]
+    dq = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
+    dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
+    dv = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
+    delta = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.hlm_attn_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+            B, T, H, Hkv, D,
+            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o),
+            _lib.strides3(dout), _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv),
+            int(window), float(scale), _stream_handle(q.device),
+        )
+    _lib.check(rc, lib)
+    return dq, dk, dv
+
+
+@hip_attn_bwd.register_fake
+def _(dout, q, k, v, o, lse, window, scale):
+    return (
+        q.new_empty(q.shape, dtype=_BF16),
+        k.new_empty(k.shape, dtype=_BF16),
+        v.new_empty(v.shape, dtype=_BF16),
+    )
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, window, scale = inputs
+    o, lse = output
+    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.window = window
+    ctx.scale = scale
+
+
+def _backward(ctx, dout, _dlse):
+    # lse is an auxiliary output for the backward; gradients flowing into it
+    # are not propagated (attention() never exposes it).
+    q, k, v, o, lse = ctx.saved_tensors
+    dq, dk, dv = hip_attn_bwd(dout, q, k, v, o, lse, ctx.window, ctx.scale)
+    return dq, dk, dv, None, None
+
+
+hip_attn_fwd.register_autograd(_backward, setup_context=_setup_context)

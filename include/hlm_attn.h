@@ -1,0 +1,88 @@
+/*
+ * hlm_attn.h -- C ABI of the MI355X (gfx950) causal sliding-window attention
+ * library libhlm_attn.so.
+ *
+ * This is the device boundary that hackable-lm's attention backends cross:
+ * the reference calls `flash_attn_func(q, k, v, dropout_p, causal=True,
+ * window_size=(W - 1, 0))` from `kernels.scaled_dot_product_attention`
+ * (/root/reference/kernels.py:836-841), reached from
+ * `AttentionCore.fwd_flash_attn_2` (/root/reference/model.py:216-226), and
+ * autograd then runs FlashAttention-2's backward.  The two entry points below
+ * replace that forward and that backward.
+ *
+ * Tensor conventions (all device pointers, caller-owned):
+ *   q, o, dO, dq          bf16 (B, T, H,   D)
+ *   k, v, dk, dv          bf16 (B, T, Hkv, D)
+ *   lse, delta_ws         fp32 (B, H, T), contiguous
+ * Each bf16 tensor has unit stride along D; its batch/time/head strides are
+ * given in ELEMENTS as int64_t[3] = {stride_b, stride_t, stride_h}.  Every
+ * stride must be a multiple of 8 and every bf16 base pointer 16-byte aligned
+ * (so rows can be moved with 128-bit accesses); v may be a strided view of a
+ * fused qkv projection (model.py:92-99).
+ *
+ * Mask: query i attends to keys j with  i - window < j <= i.
+ *   window <= 0 or window >= T  ->  plain causal (the reference's `None`
+ *   window, model.py:155-159).  This is FlashAttention's (window - 1, 0).
+ * Supported: D in {64, 128}; H % Hkv == 0 (Hkv < H is grouped-query
+ * attention); scale > 0 (the reference uses 1/sqrt(D)).
+ *
+ * Semantics: no allocation, no host synchronisation; all work is enqueued on
+ * `stream` (a hipStream_t), so calls are safe inside HIP graph capture.
+ * Return value: 0 on success, a negative HLM_ATTN_E* code otherwise; the
+ * message is available from hlm_attn_last_error() on the calling thread.
+ */
+#ifndef HLM_ATTN_H
+#define HLM_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HLM_ATTN_OK 0
+#define HLM_ATTN_EINVAL (-1)      /* bad pointer, shape, stride or alignment */
+#define HLM_ATTN_EUNSUPPORTED (-2) /* valid request this library does not implement */
+#define HLM_ATTN_ELAUNCH (-3)     /* the HIP runtime rejected a kernel launch */
+
+/* ABI revision of this header; bumped on any signature change. */
+int hlm_attn_abi_version(void);
+
+/*
+ * Forward: o = softmax(scale * q k^T + mask) v, lse = logsumexp of the same
+ * masked scores (natural log, fp32).
+ * Replaces flash_attn_func(q, k, v, dropout_p=0.0, causal=True,
+ * window_size=(window - 1, 0)) at /root/reference/kernels.py:841 and the
+ * `torch` math at /root/reference/kernels.py:785-800.
+ */
+int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                 int B, int T, int H, int Hkv, int D,
+                 const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 int window, float scale, void* stream);
+
+/*
+ * Backward: given dO and the forward's o and lse, writes dq, dk, dv (in the
+ * layouts given by their strides).  delta_ws is a caller-provided fp32
+ * (B, H, T) workspace that receives rowsum(dO * o).  dk/dv are written
+ * completely (not accumulated into).
+ * Replaces the backward of flash_attn_func (FlashAttention-2's autograd
+ * Function, called from /root/reference/kernels.py:841), i.e. the gradient
+ * of the math at /root/reference/kernels.py:785-800.
+ */
+int hlm_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
+                 int B, int T, int H, int Hkv, int D,
+                 const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                 const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                 const int64_t* dk_strides, const int64_t* dv_strides,
+                 int window, float scale, void* stream);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* hlm_attn_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HLM_ATTN_H */
