@@ -1,0 +1,349 @@
+#!/usr/bin/env python3
+"""Benchmark of the HIP causal sliding-window attention backend on one MI355X.
+
+One "step" is one attention layer's forward + backward through the C ABI
+(hlm_attn_fwd, then hlm_attn_bwd on the forward's o and lse) at the BASELINE
+workload cfg2: B=8, H=12, T=2048, D=64, window=512, causal, bf16, synthetic
+N(0,1) inputs from one seed, resident in HBM before timing starts.  Warm
+cache: steps run back to back, as in training.
+
+Prints ONE JSON line: value = effective fwd+bwd TFLOP/s, where effective FLOPs
+count only unmasked (query, key) pairs P(T, W): fwd 4*D*P, bwd 8*D*P per
+(batch, head).  Also reports ms per layer (fwd, bwd, fwd+bwd), the fraction of
+MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
+(HIP-event timed on the launch stream) and the CPU baseline: the reference's
+`torch` backend restated on the host CPU (configs[0] shape, fp32, forward).
+
+  python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "hackable-lm_amd"))
+
+METRIC = "attention fwd+bwd effective TFLOPS & % bf16 MFMA peak; ms/layer at T=2048"
+# MI355X dense bf16 MFMA peak: 256 CU x 4096 FLOP/clk x 2.4 GHz.
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    "cfg2_local": dict(B=8, T=2048, H=12, D=64, W=512),
+    "cfg3_full": dict(B=8, T=2048, H=12, D=64, W=None),
+    "cfg4_local": dict(B=4, T=4096, H=12, D=128, W=1024),
+    "cfg4_full": dict(B=4, T=4096, H=12, D=128, W=None),
+    "cfg5_long": dict(B=1, T=16384, H=16, D=128, W=2048),
+}
+CPU_CONFIG = dict(B=2, T=1024, H=6, D=64, W=256)
+
+
+def pairs(T: int, W: int | None) -> int:
+    """Unmasked (query, key) pairs per (batch, head): W(W+1)/2 + (T-W)W, or T(T+1)/2."""
+    if W is None or W >= T:
+        return T * (T + 1) // 2
+    return W * (W + 1) // 2 + (T - W) * W
+
+
+def effective_flops(cfg: dict) -> dict:
+    p = pairs(cfg["T"], cfg["W"]) * cfg["B"] * cfg["H"]
+    d = cfg["D"]
+    return {"fwd": 4 * d * p, "bwd": 8 * d * p, "bwd_dq": 2 * d * p, "bwd_dkdv": 6 * d * p}
+
+
+def algorithmic_bytes(cfg: dict) -> dict:
+    """Compulsory HBM bytes per launch (bf16 tensors, fp32 lse/delta)."""
+    n = cfg["B"] * cfg["H"] * cfg["T"]
+    d = cfg["D"]
+    return {
+        "fwd": 8 * n * d + 4 * n,               # q, k, v read; o written; lse written
+        "bwd_dq": 12 * n * d + 8 * n,           # q, k, v, o, dO read; dq written; lse read, delta written
+        "bwd_dkdv": 12 * n * d + 8 * n,         # q, k, v, dO read; dk, dv written; lse, delta read
+    }
+
+
+class Problem:
+    """Device buffers and C-ABI launches for one configuration."""
+
+    def __init__(self, cfg: dict, seed: int, device):
+        import torch
+        from hlm_attn import _lib
+
+        self.torch = torch
+        self.lib = _lib.load()
+        self.cfg = cfg
+        B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["D"]
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        mk = lambda: torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)  # noqa: E731
+        self.q, self.k, self.v, self.do = mk(), mk(), mk(), mk()
+        self.o = torch.empty_like(self.q)
+        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.lse = torch.empty(B, H, T, dtype=torch.float32, device=device)
+        self.delta = torch.empty_like(self.lse)
+        st = _lib.strides3
+        self.s = {n: st(getattr(self, n)) for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
+        self.window = 0 if cfg["W"] is None else cfg["W"]
+        self.scale = 1.0 / math.sqrt(D)
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        self.dims = (B, T, H, H, D)
+
+    def fwd(self):
+        rc = self.lib.hlm_attn_fwd(
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(), self.lse.data_ptr(),
+            *self.dims, self.s["q"], self.s["k"], self.s["v"], self.s["o"], self.window, self.scale, self.stream,
+        )
+        assert rc == 0, self.lib.hlm_attn_last_error()
+
+    def _bwd(self, fn):
+        rc = fn(
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(),
+            self.lse.data_ptr(), self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.delta.data_ptr(),
+            *self.dims, self.s["q"], self.s["k"], self.s["v"], self.s["o"], self.s["do"], self.s["dq"],
+            self.s["dk"], self.s["dv"], self.window, self.scale, self.stream,
+        )
+        assert rc == 0, self.lib.hlm_attn_last_error()
+
+    def bwd(self):
+        self._bwd(self.lib.hlm_attn_bwd)
+
+    def bwd_dq(self):
+        self._bwd(self.lib.hlm_attn_bwd_dq)
+
+    def bwd_dkdv(self):
+        self._bwd(self.lib.hlm_attn_bwd_dkdv)
+
+    def step(self):
+        self.fwd()
+        self.bwd()
+
+
+def event_time_ms(torch, fn, reps: int) -> float:
+    """Average duration of fn's launches, by HIP events on the launch stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def measure(name: str, steps: int, warmup: int, device) -> dict:
+    import torch
+
+    cfg = CONFIGS[name]
+    prob = Problem(cfg, seed=0, device=device)
+    for _ in range(warmup):
+        prob.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        prob.step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    reps = max(steps, 20)
+    kern = {
+        "fwd": event_time_ms(torch, prob.fwd, reps),
+        "bwd_dq": event_time_ms(torch, prob.bwd_dq, reps),
+        "bwd_dkdv": event_time_ms(torch, prob.bwd_dkdv, reps),
+    }
+    bwd_ms = event_time_ms(torch, prob.bwd, reps)
+    step_ms = event_time_ms(torch, prob.step, reps)
+    fl = effective_flops(cfg)
+    by = algorithmic_bytes(cfg)
+    total = fl["fwd"] + fl["bwd"]
+    dominant = max(kern, key=kern.get)
+    achieved = fl[dominant] / (kern[dominant] * 1e-3) / 1e12
+    return {
+        "cfg": cfg,
+        "wall_ms_per_step": wall_ms,
+        "event_ms_per_step": step_ms,
+        "fwd_ms": kern["fwd"],
+        "bwd_ms": bwd_ms,
+        "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
+        "tflops": {
+            "fwd": fl["fwd"] / (kern["fwd"] * 1e-3) / 1e12,
+            "bwd": fl["bwd"] / (bwd_ms * 1e-3) / 1e12,
+            "fwd_bwd": total / (wall_ms * 1e-3) / 1e12,
+            # FlashAttention convention: bwd counted as 2.5x fwd (includes the recompute).
+            "fwd_bwd_fa_convention": 3.5 * fl["fwd"] / (wall_ms * 1e-3) / 1e12,
+        },
+        "dominant": dominant,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": {"fwd": "attn_fwd_kernel", "bwd_dq": "attn_bwd_dq_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel"}[dominant],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "algorithmic_flops_per_launch": fl[dominant],
+            "algorithmic_bytes_per_launch": by[dominant],
+            "launch_us": round(kern[dominant] * 1e3, 2),
+            "traffic": read_traffic(name, dominant),
+        },
+    }
+
+
+def read_traffic(config: str, kernel: str):
+    """HBM bytes per launch of `kernel` at `config`, from the committed rocprofv3
+    PMC summary (profiles/hbm_traffic.md, lines 'traffic <config> <kernel> <bytes>')."""
+    path = REPO / "profiles" / "hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.strip().strip("`").split()
+        if len(parts) == 4 and parts[0] == "traffic" and parts[1] == config and parts[2] == kernel:
+            return int(parts[3])
+    return None
+
+
+def cpu_baseline(budget_s: float = 10.0) -> dict:
+    """The reference's `torch` backend (restated in oracle/, kernels.py:785-800)
+    on the host CPU: BASELINE configs[0], forward only, fp32."""
+    import torch
+
+    from oracle import attention as oracle
+
+    cfg = CPU_CONFIG
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(cfg["B"], cfg["T"], cfg["H"], cfg["D"], generator=g) for _ in range(3))
+    run = lambda: oracle.attention_core_torch(q, k, v, cfg["W"])  # noqa: E731
+    for _ in range(3):
+        run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    eff = 4 * cfg["D"] * pairs(cfg["T"], cfg["W"]) * cfg["B"] * cfg["H"]
+    cpu_model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(eff / med / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (
+            f"torch-backend restatement, fp32 forward, B=2 H=6 T=1024 D=64 W=256, "
+            f"median of {len(times)} runs after 3 warmups ({sum(times):.1f} s)"
+        ),
+        "ms": round(med * 1e3, 3),
+        "effective_gflop": round(eff / 1e9, 4),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg2_local", choices=sorted(CONFIGS))
+    ap.add_argument("--sweep", action="store_true", help="also time every config (printed to stderr)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument(
+        "--copy-mib", type=int, default=0,
+        help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
+        "traffic that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters",
+    )
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU: the attention kernel runs on one MI355X's share "
+            "(every (batch, head) slice is independent); multi-GPU runs are not part of this build.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    device = torch.device("cuda", 0)
+
+    if args.sweep:
+        for name in CONFIGS:
+            r = measure(name, max(10, args.steps // 2), args.warmup, device)
+            print(
+                f"{name}: fwd {r['fwd_ms']*1e3:.1f} us ({r['tflops']['fwd']:.0f} TF) | "
+                f"bwd {r['bwd_ms']*1e3:.1f} us ({r['tflops']['bwd']:.0f} TF) | "
+                f"fwd+bwd {r['wall_ms_per_step']*1e3:.1f} us ({r['tflops']['fwd_bwd']:.0f} TF, "
+                f"{100*r['tflops']['fwd_bwd']/PEAK_BF16_TFLOPS:.1f}% peak) | kernels {r['kernel_us']}",
+                file=sys.stderr,
+                flush=True,
+            )
+
+    r = measure(args.config, args.steps, args.warmup, device)
+    cfg = r["cfg"]
+    w = "causal" if cfg["W"] is None else f"window={cfg['W']}"
+    line = {
+        "metric": METRIC,
+        "value": round(r["tflops"]["fwd_bwd"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["wall_ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: one attention layer fwd+bwd, B={cfg['B']} H={cfg['H']} T={cfg['T']} "
+            f"D={cfg['D']} {w}, causal, inputs N(0,1) seed 0 resident in HBM, warm cache",
+            "B": cfg["B"],
+            "H": cfg["H"],
+            "T": cfg["T"],
+            "head_dim": cfg["D"],
+            "window": cfg["W"],
+            "parallelism": "single GPU",
+        },
+        "pct_of_bf16_peak": round(100 * r["tflops"]["fwd_bwd"] / PEAK_BF16_TFLOPS, 2),
+        "ms_per_layer": {
+            "fwd": round(r["fwd_ms"], 5),
+            "bwd": round(r["bwd_ms"], 5),
+            "fwd_bwd": round(r["wall_ms_per_step"], 5),
+        },
+        "tflops": {k: round(v, 2) for k, v in r["tflops"].items()},
+        "kernel_us": r["kernel_us"],
+        "roofline": r["roofline"],
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+    }
+    print(json.dumps(line), flush=True)
+    if args.copy_mib:
+        n = args.copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy calibration: {args.copy_mib} MiB read, {args.copy_mib} MiB written", file=sys.stderr)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

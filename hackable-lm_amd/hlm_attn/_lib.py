@@ -20,11 +20,10 @@ SIGNATURES = {
     "hlm_attn_abi_version": (_I, []),
     "hlm_attn_last_error": (ctypes.c_char_p, []),
     "hlm_attn_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _I, _F, _P]),
-    "hlm_attn_bwd": (
-        _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P],
-    ),
 }
+_BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P]
+for _name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
+    SIGNATURES[_name] = (_I, _BWD_ARGTYPES)
 
 _lib: ctypes.CDLL | None = None
 

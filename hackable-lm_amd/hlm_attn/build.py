@@ -25,6 +25,7 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA accumulators in VGPRs: no AGPR copies around the softmax
     "-Wall",
     "-Wno-unused-result",
 ]
@@ -37,10 +38,12 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False) -> Path:
-    """Compiles every kernel source into LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *(str(CSRC / s) for s in SOURCES), "-o", str(tmp)]
+def build(verbose: bool = False, out: Path | None = None, defines: tuple[str, ...] = ()) -> Path:
+    """Compiles every kernel source into LIB_PATH (always recompiles).  `out`
+    and `defines` (-D flags) build a variant elsewhere, for experiments."""
+    target = Path(out) if out is not None else LIB_PATH
+    tmp = target.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), *(str(CSRC / s) for s in SOURCES), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the device-only feature flag; drop that line.
     noise = "not a recognized feature for this target"
@@ -49,8 +52,8 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{log}")
     if verbose and log.strip():
         print(log, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":

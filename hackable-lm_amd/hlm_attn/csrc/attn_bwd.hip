@@ -310,19 +310,24 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
 }
 
 template <int D>
-hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
-  const int nqt = (a.T + 127) / 128;
-  const int64_t dq_blocks = (int64_t)nqt * a.H * a.B;
-  hipLaunchKernelGGL(attn_bwd_dq_kernel<D>, dim3((unsigned)dq_blocks), dim3(kThreads), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  const int nkt = (a.T + 127) / 128;
-  const int64_t kv_blocks = (int64_t)nkt * a.Hkv * a.B;
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, 64>), dim3((unsigned)kv_blocks), dim3(kThreads), 0, stream, a);
-  return hipGetLastError();
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
+  if (phases & kBwdDq) {
+    const int nqt = (a.T + 127) / 128;
+    const int64_t dq_blocks = (int64_t)nqt * a.H * a.B;
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<D>, dim3((unsigned)dq_blocks), dim3(kThreads), 0, stream, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (phases & kBwdDkDv) {
+    const int nkt = (a.T + 127) / 128;
+    const int64_t kv_blocks = (int64_t)nkt * a.Hkv * a.B;
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, 64>), dim3((unsigned)kv_blocks), dim3(kThreads), 0, stream, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
-template hipError_t launch_bwd<64>(const BwdArgs&, hipStream_t);
-template hipError_t launch_bwd<128>(const BwdArgs&, hipStream_t);
+template hipError_t launch_bwd<64>(const BwdArgs&, hipStream_t, int);
+template hipError_t launch_bwd<128>(const BwdArgs&, hipStream_t, int);
 
 }  // namespace hlm

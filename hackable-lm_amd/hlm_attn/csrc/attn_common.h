@@ -31,6 +31,7 @@ namespace hlm {
 typedef __bf16 bf16;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
@@ -38,6 +39,17 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kThreads = 256;  // 4 waves of 64
+
+// 32-query blocks per forward wave (1 or 2); a build-time choice.
+#ifndef HLM_FWD_QB
+#define HLM_FWD_QB 1
+#endif
+constexpr int kFwdQB = HLM_FWD_QB;
+
+// Backward phases (bit mask): dQ + delta first, then dK/dV, which reads delta.
+constexpr int kBwdDq = 1;
+constexpr int kBwdDkDv = 2;
+constexpr int kBwdAll = kBwdDq | kBwdDkDv;
 
 struct FwdArgs {
   const bf16* q;

@@ -12,7 +12,7 @@ namespace hlm {
 template <int D>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 template <int D>
-hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases);
 }  // namespace hlm
 
 namespace {
@@ -100,12 +100,15 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   return HLM_ATTN_OK;
 }
 
-int hlm_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                 const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H,
-                 int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
-                 const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
-                 const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
-                 int window, float scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int run_bwd(int phases, const void* q, const void* k, const void* v, const void* o, const void* dout,
+            const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H, int Hkv,
+            int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+            const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale, void* stream) {
   g_last_error[0] = '\0';
   int rc = check_dims(B, T, H, Hkv, D, scale);
   if (rc) return rc;
@@ -144,9 +147,27 @@ int hlm_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   a.scale = scale;
   a.scale_log2 = scale * hlm::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t err = D == 64 ? hlm::launch_bwd<64>(a, s) : hlm::launch_bwd<128>(a, s);
+  const hipError_t err = D == 64 ? hlm::launch_bwd<64>(a, s, phases) : hlm::launch_bwd<128>(a, s, phases);
   if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
   return HLM_ATTN_OK;
 }
+
+}  // namespace
+
+#define HLM_BWD_PARAMS                                                                              \
+  const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse,   \
+      void *dq, void *dk, void *dv, float *delta_ws, int B, int T, int H, int Hkv, int D,           \
+      const int64_t *q_strides, const int64_t *k_strides, const int64_t *v_strides,                 \
+      const int64_t *o_strides, const int64_t *do_strides, const int64_t *dq_strides,               \
+      const int64_t *dk_strides, const int64_t *dv_strides, int window, float scale, void *stream
+#define HLM_BWD_ARGS                                                                                \
+  q, k, v, o, dout, lse, dq, dk, dv, delta_ws, B, T, H, Hkv, D, q_strides, k_strides, v_strides,    \
+      o_strides, do_strides, dq_strides, dk_strides, dv_strides, window, scale, stream
+
+extern "C" {
+
+int hlm_attn_bwd(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdAll, HLM_BWD_ARGS); }
+int hlm_attn_bwd_dq(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDq, HLM_BWD_ARGS); }
+int hlm_attn_bwd_dkdv(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDkDv, HLM_BWD_ARGS); }
 
 }  // extern "C"

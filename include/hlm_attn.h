@@ -78,6 +78,28 @@ int hlm_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  const int64_t* dk_strides, const int64_t* dv_strides,
                  int window, float scale, void* stream);
 
+/*
+ * The two phases of hlm_attn_bwd, same arguments, run in this order on one
+ * stream: hlm_attn_bwd_dq writes dq and delta_ws; hlm_attn_bwd_dkdv reads
+ * delta_ws and writes dk, dv.  hlm_attn_bwd == dq phase then dkdv phase.
+ * Exposed so a caller can time or schedule the phases separately; the
+ * reference has no counterpart (FlashAttention-2's backward is one call).
+ */
+int hlm_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                    const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
+                    int B, int T, int H, int Hkv, int D,
+                    const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                    const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                    const int64_t* dk_strides, const int64_t* dv_strides,
+                    int window, float scale, void* stream);
+int hlm_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                      const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
+                      int B, int T, int H, int Hkv, int D,
+                      const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                      const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                      const int64_t* dk_strides, const int64_t* dv_strides,
+                      int window, float scale, void* stream);
+
 /* Message describing the last failed call on this thread ("" if none). */
 const char* hlm_attn_last_error(void);
 

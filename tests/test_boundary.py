@@ -1,0 +1,260 @@
+"""CPU tests of the drop-in boundary: the C ABI library and its Python mirror
+of the reference's backend interface.  Nothing here launches a kernel.
+
+The dispatch tests follow the reference's own fake-kernel tests
+(tests/test_kernels.py:133-226: fake flash_attn_func handles pin the bf16
+cast, causal flag, window mapping and bf16 output); here a fake custom op
+stands in for the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import hlm_attn
+from hlm_attn import _lib, config, kernels, model, ops
+from oracle import attention as oracle
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "hlm_attn.h"
+
+
+def declared_symbols() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(hlm_attn_\w+)\s*\(", text))
+
+
+# --- the shared library -------------------------------------------------------
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert {"hlm_attn_fwd", "hlm_attn_bwd", "hlm_attn_last_error", "hlm_attn_abi_version"} <= names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(_lib.SIGNATURES) == names, "ctypes binding and header disagree"
+    assert lib.hlm_attn_abi_version() == _lib.ABI_VERSION
+
+
+def _strides(*s):
+    return (ctypes.c_int64 * 3)(*s)
+
+
+def _fwd(lib, ptr=0x1000, B=1, T=16, H=2, Hkv=2, D=64, strides=(2048, 128, 64), window=0, scale=0.125):
+    s = _strides(*strides)
+    p = ctypes.c_void_p(ptr) if ptr else None
+    lse = ctypes.c_void_p(0x2000)
+    return lib.hlm_attn_fwd(p, p, p, p, lse, B, T, H, Hkv, D, s, s, s, s, window, scale, None)
+
+
+@pytest.mark.parametrize(
+    "kwargs,code,msg",
+    [
+        (dict(D=96), -2, "head_dim 96"),
+        (dict(D=32), -2, "head_dim 32"),
+        (dict(H=3, Hkv=2), -1, "not a multiple"),
+        (dict(H=0), -1, "bad shape"),
+        (dict(ptr=None), -1, "null pointer"),
+        (dict(ptr=0x1008), -1, "16-byte aligned"),
+        (dict(strides=(2048, 100, 64)), -1, "multiple of 8"),
+        (dict(strides=(-8, 128, 64)), -1, "multiple of 8"),
+        (dict(scale=0.0), -1, "scale"),
+        (dict(scale=float("nan")), -1, "scale"),
+    ],
+)
+def test_fwd_rejects_bad_arguments_before_touching_the_device(kwargs, code, msg):
+    lib = _lib.load()
+    assert _fwd(lib, **kwargs) == code
+    assert msg in lib.hlm_attn_last_error().decode()
+
+
+def test_empty_problems_are_no_ops():
+    lib = _lib.load()
+    assert _fwd(lib, B=0) == 0
+    assert _fwd(lib, T=0) == 0
+    assert lib.hlm_attn_last_error() == b""
+
+
+def test_bwd_phases_validate_like_bwd():
+    lib = _lib.load()
+    s = _strides(2048, 128, 64)
+    p = ctypes.c_void_p(0x1000)
+    for name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
+        fn = getattr(lib, name)
+        rc = fn(p, p, p, p, p, p, p, p, p, None, 1, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None)
+        assert rc == -1 and b"delta_ws" in lib.hlm_attn_last_error()
+        rc = fn(p, p, p, p, p, p, p, p, p, p, 1, 16, 2, 2, 128 + 8, s, s, s, s, s, s, s, s, 0, 0.125, None)
+        assert rc == -2
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.HipAttentionUnavailable, match="build it"):
+        _lib.load(tmp_path / "libhlm_attn.so")
+
+
+# --- torch custom ops --------------------------------------------------------------
+
+def test_ops_refuse_cpu_tensors():
+    q = torch.randn(1, 8, 2, 64).bfloat16()
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        ops.hip_attn_fwd(q, q, q, 0, 0.125)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        hlm_attn.attention(q.float(), q.float(), q.float())
+
+
+def test_fake_implementations_describe_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(2, 40, 8, 64, dtype=torch.bfloat16)
+        k = torch.empty(2, 40, 2, 64, dtype=torch.bfloat16)
+        o, lse = ops.hip_attn_fwd(q, k, k, 16, 0.125)
+        assert o.shape == q.shape and o.dtype == torch.bfloat16
+        assert lse.shape == (2, 8, 40) and lse.dtype == torch.float32
+        dq, dk, dv = ops.hip_attn_bwd(q, q, k, k, o, lse, 16, 0.125)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+
+
+def test_kernel_ready_keeps_aligned_views_and_copies_the_rest():
+    qkv = torch.randn(2, 10, 3 * 4 * 64).bfloat16()
+    v = qkv[..., 2 * 256 :].view(2, 10, 4, 64)  # a fused-projection view, as model.py:92-99 makes
+    assert ops._kernel_ready(v) is v
+    t = torch.randn(2, 10, 4, 64).bfloat16().transpose(2, 3).contiguous().transpose(2, 3)
+    assert t.stride(3) != 1 and ops._kernel_ready(t).is_contiguous()
+    odd = torch.randn(2, 10, 4, 68).bfloat16()[..., :64]  # row stride 68: not a multiple of 8
+    assert ops._kernel_ready(odd).is_contiguous()
+
+
+# --- dispatch, with a fake op standing in for the kernels ----------------------------
+
+class FakeOp:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, q, k, v, window, scale):
+        self.calls.append((q.dtype, k.dtype, v.dtype, q.shape, k.shape, window, scale))
+        B, T, H, D = q.shape
+        return q.bfloat16(), torch.zeros(B, H, T)
+
+
+@pytest.fixture()
+def fake_op(monkeypatch):
+    fake = FakeOp()
+    monkeypatch.setattr(ops, "hip_attn_fwd", fake)
+    return fake
+
+
+def test_sdpa_casts_to_bf16_and_maps_window(fake_op):
+    """The hip branch mirrors the FA2 branch (kernels.py:836-841): bf16 inputs,
+    causal, window W means keys i-W+1..i (FA's (W-1, 0)), bf16 output, GQA k."""
+    q = torch.randn(2, 4, 3, 64)
+    k = torch.randn(2, 4, 1, 64)
+    out = kernels.scaled_dot_product_attention(q, k, k, dropout_p=0.0, is_causal=True, window_size=3, backend="hip")
+    assert out.dtype == torch.bfloat16
+    assert fake_op.calls == [(torch.bfloat16, torch.bfloat16, torch.bfloat16, q.shape, k.shape, 3, 64**-0.5)]
+    kernels.scaled_dot_product_attention(q, k, k, dropout_p=0.0, window_size=None, backend="hip")
+    assert fake_op.calls[-1][5] == 0  # no window -> plain causal
+
+
+@pytest.mark.parametrize(
+    "kwargs,match",
+    [
+        (dict(dropout_p=0.1), "dropout"),
+        (dict(attn_mask=torch.ones(4, 4, dtype=torch.bool)), "explicit attention mask"),
+        (dict(block_mask=object()), "explicit attention mask"),
+        (dict(is_causal=False), "causal attention only"),
+        (dict(backend="flash_attn_2"), "implements only"),
+    ],
+)
+def test_sdpa_rejects_what_the_kernels_do_not_do(fake_op, kwargs, match):
+    q = torch.randn(1, 4, 2, 64)
+    args = dict(dropout_p=0.0)
+    args.update(kwargs)
+    with pytest.raises(RuntimeError, match=match):
+        kernels.scaled_dot_product_attention(q, q, q, **args)
+    assert fake_op.calls == []
+
+
+def test_attention_core_uses_layer_pattern(fake_op):
+    cfg = model.AttentionConfig(n_layer=8, n_head=2, n_kv_head=2, attention_window=4, attention_full_every=4)
+    cores = [model.AttentionCore(cfg, i) for i in range(8)]
+    assert [c.attention_window for c in cores] == [4, 4, 4, None, 4, 4, 4, None]
+    q = torch.randn(1, 8, 2, 64)
+    out = cores[0](q, q, q)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    assert fake_op.calls[-1][5] == 4
+    cores[3](q, q, q)
+    assert fake_op.calls[-1][5] == 0
+    # W >= T is plain causal (model.py:155-159)
+    cores[0](q[:, :4], q[:, :4], q[:, :4])
+    assert fake_op.calls[-1][5] == 0
+    cores[0].train()
+    cores[0].dropout = 0.1
+    with pytest.raises(RuntimeError, match="dropout"):
+        cores[0](q, q, q)
+
+
+def test_attention_core_rejects_unknown_backend():
+    cfg = model.AttentionConfig(n_layer=2, n_head=2, n_kv_head=2, attention_backend="sdpa")
+    core = model.AttentionCore(cfg, 0)
+    with pytest.raises(ValueError, match="unknown attention_backend"):
+        core(torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64))
+    cfg2 = model.AttentionConfig(n_layer=2, n_head=2, n_kv_head=2, attention_backend="flash_attn_2")
+    with pytest.raises(RuntimeError, match="does not support backend"):
+        model.AttentionCore(cfg2, 0)(torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64))
+
+
+# --- config mirror -----------------------------------------------------------------
+
+def test_backend_names_extend_the_reference_set():
+    assert config.REFERENCE_ATTENTION_BACKENDS == {"torch", "flex_attention", "flash_attn_2", "flash_attn_3", "flash_attn_4"}
+    assert config.ATTENTION_BACKENDS == config.REFERENCE_ATTENTION_BACKENDS | {"hip"}
+    assert config.normalize_attention_backend("HIP") == "hip"
+    for bad in ("sdpa", 3, None):
+        with pytest.raises(ValueError, match="unknown attention_backend"):
+            config.normalize_attention_backend(bad)
+
+
+def test_layer_pattern_matches_oracle_restatement():
+    assert [config.layer_attention_window(i, 8, 512, 4) for i in range(8)] == [512, 512, 512, None, 512, 512, 512, None]
+    assert [config.layer_attention_window(i, 3, 512, 4) for i in range(3)] == [512, 512, None]
+    for n in range(1, 20):
+        for w in (None, 64, 512):
+            for every in (None, 1, 3, 4):
+                assert [config.layer_attention_window(i, n, w, every) for i in range(n)] == [
+                    oracle.layer_attention_window(i, n, w, every) for i in range(n)
+                ]
+    assert config.normalize_attention_window(0) is None and config.normalize_attention_window(512) == 512
+    assert config.normalize_attention_full_every(0) is None and config.normalize_attention_full_every(4) == 4
+    for T in (1, 7, 8, 9):
+        assert config.attention_window_size(8, T) == oracle.window_size_at(8, T)
+
+
+def test_resolution_follows_the_reference_rules(monkeypatch):
+    """kernels.py:177-181 and :221-228: raise when the fast backend is
+    unusable, or fall back to the host's torch backend when allowed."""
+    monkeypatch.setattr(kernels, "hip_attention_available", lambda: False)
+    with pytest.raises(RuntimeError, match="attention_backend=hip"):
+        kernels.resolve_attention_backend("hip")
+    assert kernels.resolve_attention_backend("hip", allow_torch_backend=True) == "torch"
+    assert kernels.resolve_attention_backend("flash_attn_2") == "flash_attn_2"
+    monkeypatch.setattr(kernels, "hip_attention_available", lambda: True)
+    assert kernels.resolve_attention_backend("HIP") == "hip"
+    with pytest.raises(ValueError):
+        kernels.resolve_attention_backend("sdpa")
+
+
+def test_flop_model_matches_bench():
+    import bench
+
+    for T, W in [(2048, 512), (2048, None), (4096, 1024), (16384, 2048), (1024, 256)]:
+        assert bench.pairs(T, W) == oracle.causal_window_pairs(T, W)
+    f = bench.effective_flops(bench.CONFIGS["cfg2_local"])
+    assert round(f["fwd"] / 1e9, 3) == 22.555 and round(f["bwd"] / 1e9, 3) == 45.110
+    assert f["bwd_dq"] + f["bwd_dkdv"] == f["bwd"]
+    assert math.isclose(bench.PEAK_BF16_TFLOPS, 256 * 4096 * 2.4e9 / 1e12, rel_tol=1e-4)
