@@ -72,7 +72,7 @@ struct BwdArgs {
   bf16* dq;
   bf16* dk;
   bf16* dv;
-  float* delta;  // (B, H, T) workspace: rowsum(dO * O), written by the dq kernel
+  float* delta;  // 2 x (B, H, T) workspace written by the dq kernel: rowsum(dO * O), then lse * log2(e)
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3];
   int B, T, H, Hkv, W;
   float scale;       // softmax scale
@@ -137,38 +137,101 @@ __device__ __forceinline__ bf16x8 lds_operand_tr(const bf16* x, int stride, int 
   return out;
 }
 
-// Global -> register -> LDS copy of a ROWS x D bf16 tile (row-major in both
-// places, LDS row stride D + 8 elements).  Rows at or beyond `nrows` read as 0.
-// Each thread moves 16-byte chunks; consecutive threads take consecutive
-// chunks of a row, so every global access is a coalesced 128-bit load.
-template <int ROWS, int D>
-struct RowTile {
-  static constexpr int kChunksPerRow = D / 8;
-  static constexpr int kChunks = ROWS * kChunksPerRow;
-  static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
-  static constexpr bool kExact = (kChunks % kThreads) == 0;
-  uint4 r[kPer];
+typedef __attribute__((address_space(3))) void lds_void;
 
-  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int r0, int nrows,
-                                       int tid) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c / kChunksPerRow, col = (c % kChunksPerRow) * 8;
-      r[i] = make_uint4(0u, 0u, 0u, 0u);
-      if ((kExact || c < kChunks) && r0 + row < nrows)
-        r[i] = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + row) * row_stride + col);
-    }
-  }
+// Buffer resource over one (batch, head) slab of a (B, T, H, D) tensor: T rows
+// of 2*D bytes at a row stride of `st` elements.  Loads beyond the slab's last
+// byte return zeros (checked on the MI355X), so tile loads need no bounds
+// branches: rows >= T simply arrive as zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16* base, int64_t st, int T, int D) {
+  const int64_t extent = (int64_t)(T - 1) * st * 2 + 2 * D;  // bytes; < 2^31 (checked by the host)
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
+}
 
-  __device__ __forceinline__ void store(bf16* lds, int tid) const {
+// 16 bytes of one row at element column `col` through a slab resource.
+__device__ __forceinline__ bf16x8 slab_load(__amdgpu_buffer_rsrc_t rs, int row, int st2, int col) {
+  typedef __attribute__((ext_vector_type(4))) int i32x4;
+  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, row * st2 + col * 2, 0, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// One LDS DMA instruction: `bytes` (16 or 4) per lane from the buffer at byte
+// offset voff into lds + bytes * lane (lane placement checked on the MI355X).
+// Issued as inline asm on purpose: the compiler then does not track these LDS
+// writes, so it inserts no conservative vmcnt waits before unrelated LDS
+// reads; every wait for them is explicit (dma_barrier).  Vector-memory loads
+// complete in issue order, so the compiler's own waits for its loads can only
+// over-wait.
+template <int bytes>
+__device__ __forceinline__ void lds_dma(__amdgpu_buffer_rsrc_t rs, const void* lds, int voff) {
+  const unsigned ldsaddr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void*)lds);
+  if constexpr (bytes == 16)
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
+  else
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
+}
+
+// Direct buffer -> LDS copies of a ROWS x D tile starting at row r0 (st2 = row
+// stride in bytes).  Each instruction moves 1 KB, and a layout is chosen by
+// choosing each lane's source address.  The NW waves of a workgroup split the
+// 1 KB pieces among themselves; nothing passes through VGPRs.
+//
+// Row-major: rows are contiguous (2*D bytes each), for ds_read_b64_tr_b16.
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ void dma_rows(__amdgpu_buffer_rsrc_t rs, int st2, int r0, bf16* lds, int wave, int lane) {
+  constexpr int NI = ROWS * D / 512, LPR = D / 8;  // 1 KB pieces; lanes per row
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c / kChunksPerRow, col = (c % kChunksPerRow) * 8;
-      if (kExact || c < kChunks) *reinterpret_cast<uint4*>(lds + row * (D + 8) + col) = r[i];
-    }
+  for (int i = 0; i < NI / NW; ++i) {
+    const int j = wave + NW * i;
+    const int row = r0 + j * (64 / LPR) + lane / LPR;
+    lds_dma<16>(rs, lds + j * 512, row * st2 + (lane % LPR) * 16);
   }
-};
+}
+
+// Fragment-major: piece f = rb * (D / 16) + s holds, in lane order l, the
+// 16 bytes of row 32 rb + l % 32 at columns 16 s + 8 (l / 32) .. + 7 -- exactly
+// the A/B operand of one 32x32x16 MFMA -- so an operand read is one contiguous
+// 1 KB ds_read_b128 (frag_operand).
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ void dma_frags(__amdgpu_buffer_rsrc_t rs, int st2, int r0, bf16* lds, int wave, int lane) {
+  constexpr int NI = ROWS * D / 512, SPR = D / 16;  // 1 KB pieces; pieces per 32-row block
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
+#pragma unroll
+  for (int i = 0; i < NI / NW; ++i) {
+    const int j = wave + NW * i;
+    const int row = r0 + 32 * (j / SPR) + (lane & 31);
+    const int col = 16 * (j % SPR) + 8 * (lane >> 5);
+    lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
+  }
+}
+
+// Barrier for tiles that arrive by LDS DMA: wait until at most `pending` of
+// this wave's vector-memory ops are outstanding (the DMA of newer tiles,
+// which complete after the older ones), drain LDS ops, then s_barrier.  A
+// plain __syncthreads() would drain every outstanding DMA, which removes the
+// prefetch depth.  Callers make sure no stores are in flight when they rely
+// on `pending` counting only DMA loads.
+template <int pending>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(pending >= 0 && pending < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (0) | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((pending & 15) | (7 << 4) | ((pending >> 4) << 14));
+  asm volatile("" ::: "memory");  // no compiler motion of memory ops across the barrier
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Waits for every outstanding vector-memory op of this wave.  Used once after
+// a kernel's prologue loads (and stores), so that inside the DMA-pipelined
+// loop the compiler has nothing of its own left to wait for and dma_barrier's
+// counts cover exactly the DMA of newer tiles.
+__device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// Operand (rb, s) of a fragment-major tile.
+template <int D>
+__device__ __forceinline__ bf16x8 frag_operand(const bf16* lds, int rb, int s, int lane) {
+  return *reinterpret_cast<const bf16x8*>(lds + (rb * (D / 16) + s) * 512 + lane * 8);
+}
 
 }  // namespace hlm

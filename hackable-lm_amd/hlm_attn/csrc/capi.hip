@@ -30,7 +30,12 @@ int fail(int code, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_tensor(const char* name, const void* p, const int64_t* s) {
+// The kernels address rows of one (batch, head) slab through buffer
+// resources with 32-bit byte offsets: (T + 512) rows at the time stride must
+// stay below 2^31 bytes.  Rows must not overlap (time stride >= D): then every
+// row at or beyond T lies outside the slab and reads as zeros, which the
+// kernels rely on instead of masking padded rows.
+int check_tensor(const char* name, const void* p, const int64_t* s, int T, int D) {
   if (p == nullptr) return fail(HLM_ATTN_EINVAL, "%s is a null pointer", name);
   if (!aligned16(p)) return fail(HLM_ATTN_EINVAL, "%s is not 16-byte aligned", name);
   if (s == nullptr) return fail(HLM_ATTN_EINVAL, "%s strides are a null pointer", name);
@@ -38,6 +43,9 @@ int check_tensor(const char* name, const void* p, const int64_t* s) {
     if (s[i] < 0 || s[i] % 8 != 0)
       return fail(HLM_ATTN_EINVAL, "%s stride[%d] = %lld must be a non-negative multiple of 8 elements",
                   name, i, (long long)s[i]);
+  if (s[1] < D) return fail(HLM_ATTN_EINVAL, "%s time stride %lld is below head_dim %d", name, (long long)s[1], D);
+  if (((int64_t)T + 512) * s[1] * 2 >= ((int64_t)1 << 31))
+    return fail(HLM_ATTN_EUNSUPPORTED, "%s: T x time stride too large for 32-bit row offsets", name);
   return HLM_ATTN_OK;
 }
 
@@ -62,7 +70,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 1; }
+int hlm_attn_abi_version(void) { return 2; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -74,8 +82,8 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   int rc = check_dims(B, T, H, Hkv, D, scale);
   if (rc) return rc;
   if (B == 0 || T == 0) return HLM_ATTN_OK;
-  if ((rc = check_tensor("q", q, q_strides)) || (rc = check_tensor("k", k, k_strides)) ||
-      (rc = check_tensor("v", v, v_strides)) || (rc = check_tensor("o", o, o_strides)))
+  if ((rc = check_tensor("q", q, q_strides, T, D)) || (rc = check_tensor("k", k, k_strides, T, D)) ||
+      (rc = check_tensor("v", v, v_strides, T, D)) || (rc = check_tensor("o", o, o_strides, T, D)))
     return rc;
   if (lse == nullptr) return fail(HLM_ATTN_EINVAL, "lse is a null pointer");
   hlm::FwdArgs a;
@@ -113,10 +121,10 @@ int run_bwd(int phases, const void* q, const void* k, const void* v, const void*
   int rc = check_dims(B, T, H, Hkv, D, scale);
   if (rc) return rc;
   if (B == 0 || T == 0) return HLM_ATTN_OK;
-  if ((rc = check_tensor("q", q, q_strides)) || (rc = check_tensor("k", k, k_strides)) ||
-      (rc = check_tensor("v", v, v_strides)) || (rc = check_tensor("o", o, o_strides)) ||
-      (rc = check_tensor("dout", dout, do_strides)) || (rc = check_tensor("dq", dq, dq_strides)) ||
-      (rc = check_tensor("dk", dk, dk_strides)) || (rc = check_tensor("dv", dv, dv_strides)))
+  if ((rc = check_tensor("q", q, q_strides, T, D)) || (rc = check_tensor("k", k, k_strides, T, D)) ||
+      (rc = check_tensor("v", v, v_strides, T, D)) || (rc = check_tensor("o", o, o_strides, T, D)) ||
+      (rc = check_tensor("dout", dout, do_strides, T, D)) || (rc = check_tensor("dq", dq, dq_strides, T, D)) ||
+      (rc = check_tensor("dk", dk, dk_strides, T, D)) || (rc = check_tensor("dv", dv, dv_strides, T, D)))
     return rc;
   if (lse == nullptr) return fail(HLM_ATTN_EINVAL, "lse is a null pointer");
   if (delta_ws == nullptr) return fail(HLM_ATTN_EINVAL, "delta_ws is a null pointer");

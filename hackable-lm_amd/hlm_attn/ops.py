@@ -22,12 +22,13 @@ _BF16 = torch.bfloat16
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """Returns t if its layout fits the kernels (unit D stride, 16-byte aligned
-    rows), else a contiguous copy."""
+    """Returns t if its layout fits the kernels (unit D stride, 16-byte aligned,
+    non-overlapping rows), else a contiguous copy."""
     s = t.stride()
     ok = (
         s[3] == 1
         and all(x >= 0 and x % 8 == 0 for x in s[:3])
+        and s[1] >= t.shape[3]
         and t.data_ptr() % 16 == 0
     )
     return t if ok else t.contiguous()
@@ -106,7 +107,7 @@ def hip_attn_bwd(
     dq = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
     dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     dv = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
-    delta = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # rowsum(dO*O), lse*log2(e)
     with torch.cuda.device(q.device):
         rc = lib.hlm_attn_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),

@@ -13,12 +13,15 @@
  * Tensor conventions (all device pointers, caller-owned):
  *   q, o, dO, dq          bf16 (B, T, H,   D)
  *   k, v, dk, dv          bf16 (B, T, Hkv, D)
- *   lse, delta_ws         fp32 (B, H, T), contiguous
+ *   lse                   fp32 (B, H, T), contiguous
+ *   delta_ws              fp32 workspace of 2 * B * H * T floats
  * Each bf16 tensor has unit stride along D; its batch/time/head strides are
  * given in ELEMENTS as int64_t[3] = {stride_b, stride_t, stride_h}.  Every
  * stride must be a multiple of 8 and every bf16 base pointer 16-byte aligned
- * (so rows can be moved with 128-bit accesses); v may be a strided view of a
- * fused qkv projection (model.py:92-99).
+ * (so rows can be moved with 128-bit accesses), stride_t >= D (rows do not
+ * overlap), and (T + 512) * stride_t * 2 must stay below 2^31 (rows are
+ * addressed with 32-bit byte offsets); v may be a strided view of a fused
+ * qkv projection (model.py:92-99).
  *
  * Mask: query i attends to keys j with  i - window < j <= i.
  *   window <= 0 or window >= T  ->  plain causal (the reference's `None`
@@ -64,8 +67,9 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 /*
  * Backward: given dO and the forward's o and lse, writes dq, dk, dv (in the
  * layouts given by their strides).  delta_ws is a caller-provided fp32
- * (B, H, T) workspace that receives rowsum(dO * o).  dk/dv are written
- * completely (not accumulated into).
+ * workspace of 2 * B * H * T floats: it receives rowsum(dO * o), then
+ * lse * log2(e), each as (B, H, T).  dk/dv are written completely (not
+ * accumulated into).
  * Replaces the backward of flash_attn_func (FlashAttention-2's autograd
  * Function, called from /root/reference/kernels.py:841), i.e. the gradient
  * of the math at /root/reference/kernels.py:785-800.
