@@ -66,8 +66,8 @@ def algorithmic_bytes(cfg: dict) -> dict:
     d = cfg["D"]
     return {
         "fwd": 8 * n * d + 4 * n,               # q, k, v read; o written; lse written
-        "bwd_dq": 12 * n * d + 12 * n,          # q, k, v, o, dO read; dq written; lse read; delta, lse2 written
-        "bwd_dkdv": 12 * n * d + 8 * n,         # q, k, v, dO read; dk, dv written; lse2, delta read
+        "bwd_dq": 12 * n * d + 12 * n,          # q, k, v, o, dO read; dq written; lse read; -lse*log2(e), -delta written
+        "bwd_dkdv": 12 * n * d + 8 * n,         # q, k, v, dO read; dk, dv written; -lse*log2(e), -delta read
     }
 
 
@@ -88,7 +88,7 @@ class Problem:
         self.o = torch.empty_like(self.q)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
         self.lse = torch.empty(B, H, T, dtype=torch.float32, device=device)
-        self.delta = torch.empty(2, B, H, T, dtype=torch.float32, device=device)  # delta, lse*log2(e)
+        self.delta = torch.empty(2, B, H, T, dtype=torch.float32, device=device)  # -lse*log2(e), -delta
         st = _lib.strides3
         self.s = {n: st(getattr(self, n)) for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
         self.window = 0 if cfg["W"] is None else cfg["W"]

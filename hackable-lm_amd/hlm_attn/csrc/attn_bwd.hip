@@ -7,31 +7,62 @@
 // i.e. the autograd of hackable-lm's `torch` backend (kernels.py:785-800),
 // with P recomputed from the saved lse instead of stored.
 //
-// Two kernels, no atomics (fp32 atomics run at ~1.36 TB/s on the MI355X,
-// far too slow to accumulate dQ across key tiles):
-//   attn_bwd_dq_kernel    query-stationary.  Writes delta and lse * log2(e)
-//                         (the workspace the next kernel reads) and dQ.
-//   attn_bwd_dkdv_kernel  key-stationary: 64 keys per wave, 256 per
+// Two kernels, no atomics (fp32 atomics run at ~1.3 TB/s on the MI355X, far
+// too slow to accumulate dQ across key blocks):
+//   attn_bwd_dq_kernel    query-stationary, 32 queries per wave.  Writes the
+//                         workspace the next kernel reads (-lse * log2(e) and
+//                         -delta per query row) and dQ.
+//   attn_bwd_dkdv_kernel  key-stationary, 32 keys per wave, 128 per
 //                         workgroup, for one kv head; loops over the query
-//                         heads of its group and the query tiles that can see
-//                         its keys, accumulating dK and dV in registers.
-// Both skip whole tiles outside the causal window, so cost scales with T * W.
-// Tiles reach LDS by buffer DMA into named buffers (triple-buffered, loop
-// unrolled by three), fragment-major for operands read along their rows and
-// row-major for operands read transposed with ds_read_b64_tr_b16.
+//                         heads of its group and the 32-row query tiles that
+//                         can see its keys, accumulating dK and dV in VGPRs.
+// Both skip whole tiles outside the causal window, so cost scales with T * W,
+// and both fit two waves per SIMD (at most 256 VGPRs).
+//
+// Per score element the VALU does two operations (exp2, multiply) plus two
+// half bf16 conversions:
+// * the stationary operand that meets the moving one in S (Q in the dq kernel,
+//   K in the dkdv kernel) is held pre-multiplied by scale * log2(e), rounded
+//   to bf16, so S comes out in log2 units;
+// * the S and dP accumulators start from -lse * log2(e) and -delta instead of
+//   zero, so the MFMAs deliver S - lse and dP - delta directly, and
+//   P = exp2(acc), dS = P * acc;
+// * on tiles that cross the diagonal or the window edge, masked entries of the
+//   S accumulator's start value are set to -inf (P = 0 there), before the
+//   MFMAs and independent of them.
+// Tiles reach LDS by buffer DMA into named buffers (triple- or double-
+// buffered, loop unrolled accordingly), fragment-major for operands read along
+// their rows and row-major for operands read transposed with
+// ds_read_b64_tr_b16.
 #include "attn_common.h"
 
 namespace hlm {
 
+// bf16 round of x * f, elementwise.
+__device__ __forceinline__ bf16x8 scale_bf16x8(bf16x8 x, float f) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)((float)x[e] * f);
+  return r;
+}
+
+__device__ __forceinline__ f32x16 splat16(float v) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = v;
+  return r;
+}
+
 // ---------------------------------------------------------------------------
-// dQ (+ delta, lse2).  Same orientation as the forward: per wave, lanes own
-// query columns of S^T = K Q^T and dP^T = V dO^T, so lse and delta are
-// per-lane scalars; dQ^T += K^T dS^T reads K^T transposed from the row-major
-// copy of the K tile.
+// dQ (+ the workspace).  Same orientation as the forward: per wave, lanes own
+// query columns of S^T = K Q^T and dP^T = V dO^T, so -lse * log2(e) and
+// -delta are per-lane constants (splat start values of the accumulators);
+// dQ^T += K^T dS^T reads K^T transposed from the row-major copy of the K tile.
 // ---------------------------------------------------------------------------
-template <int D, int QB>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
-  constexpr int NW = 4, QW = 32 * QB, BM = NW * QW, BN = 64;
+template <int D, int BN>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
+  constexpr int NW = 4, BM = NW * 32;
+  constexpr int KB = BN / 32, NDB = D / 32, NS = D / 16;
   constexpr int TILE = BN * D;
   constexpr int PER = 3 * TILE / 512 / NW;  // DMA instructions per wave per tile
   __shared__ __attribute__((aligned(1024))) bf16 kf0[TILE];
@@ -54,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h32 = lane >> 5;
-  const int q0 = qt * BM, qw0 = q0 + QW * wave;
+  const int q0 = qt * BM, qw0 = q0 + 32 * wave, myq = qw0 + l32;
 
   const __amdgpu_buffer_rsrc_t rq = slab_rsrc(a.q + b * a.sq[0] + h * a.sq[2], a.sq[1], T, D);
   const __amdgpu_buffer_rsrc_t rdo = slab_rsrc(a.dout + b * a.sdo[0] + h * a.sdo[2], a.sdo[1], T, D);
@@ -63,6 +94,28 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
   const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2), so2 = (int)(a.so[1] * 2);
   const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
+  const float c = a.scale_log2;
+
+  // Q^T (times scale * log2(e)) and dO^T as B operands: lane l holds row
+  // qw0 + l % 32, columns 16 s + 8 (l / 32) + e.  Rows >= T read as zeros.
+  bf16x8 qreg[NS], doreg[NS];
+  float dpart = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int col = 16 * s + 8 * h32;
+    qreg[s] = scale_bf16x8(slab_load(rq, myq, sq2, col), c);
+    doreg[s] = slab_load(rdo, myq, sdo2, col);
+    const bf16x8 o8 = slab_load(ro, myq, so2, col);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dpart += (float)doreg[s][e] * (float)o8[e];
+  }
+  const float ndelta = -(dpart + __shfl_xor(dpart, 32));
+  const float nlse2 = myq < T ? -a.lse[(int64_t)bh * T + myq] * kLog2e : 0.f;
+  if (myq < T && h32 == 0) {
+    a.delta[(int64_t)bh * T + myq] = nlse2;
+    a.delta[(int64_t)(a.B * H + bh) * T + myq] = ndelta;
+  }
+  drain_vmem();
 
   const int key_lo = max(0, q0 - W + 1);
   const int key_hi = min(T, q0 + BM) - 1;
@@ -72,92 +125,56 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
     dma_rows<BN, D, NW>(rk, sk2, t * BN, kr, wave, lane);
     dma_frags<BN, D, NW>(rv, sv2, t * BN, vf, wave, lane);
   };
-
-  bf16x8 qreg[QB][D / 16], doreg[QB][D / 16];
-  float delta[QB], lse2[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int myq = qw0 + 32 * qb + l32;
-    float dpart = 0.f;
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const int col = 16 * s + 8 * h32;
-      qreg[qb][s] = slab_load(rq, myq, sq2, col);
-      doreg[qb][s] = slab_load(rdo, myq, sdo2, col);
-      const bf16x8 o8 = slab_load(ro, myq, so2, col);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dpart += (float)doreg[qb][s][e] * (float)o8[e];
-    }
-    delta[qb] = dpart + __shfl_xor(dpart, 32);
-    lse2[qb] = myq < T ? a.lse[(int64_t)bh * T + myq] * kLog2e : 0.f;
-    if (myq < T && h32 == 0) {
-      a.delta[(int64_t)bh * T + myq] = delta[qb];
-      a.delta[(int64_t)(a.B * H + bh) * T + myq] = lse2[qb];
-    }
-  }
-  drain_vmem();
   load_tile(t_lo, kf0, kr0, vf0);
   if (t_lo + 1 <= t_hi) load_tile(t_lo + 1, kf1, kr1, vf1);
 
-  f32x16 dqacc[QB][D / 32];
+  f32x16 dqacc[NDB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) dqacc[qb][db] = zero16();
+  for (int db = 0; db < NDB; ++db) dqacc[db] = zero16();
+  const f32x16 sinit = splat16(nlse2), dinit = splat16(ndelta);
 
   const bool wave_live = qw0 < T;
-  const int wq_hi = min(qw0 + QW - 1, T - 1);
-  const float c = a.scale_log2;
+  const int wq_hi = min(qw0 + 31, T - 1);
 
   auto tile_step = [&](const int t, const bf16* kf, const bf16* kr, const bf16* vf) __attribute__((always_inline)) {
-    const int k0 = t * BN;
-    if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) return;
-    const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + QW - W);
 #pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb) {
-      f32x16 sacc[QB], pacc[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        sacc[qb] = zero16();
-        pacc[qb] = zero16();
-      }
-#pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        const bf16x8 kop = frag_operand<D>(kf, kb, s, lane);
-        const bf16x8 vop = frag_operand<D>(vf, kb, s, lane);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          sacc[qb] = mfma32(kop, qreg[qb][s], sacc[qb]);
-          pacc[qb] = mfma32(vop, doreg[qb][s], pacc[qb]);
-        }
-      }
-      bf16x8 dsb[QB][2];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const int d0 = qw0 + 32 * qb + l32 - k0 - 32 * kb - 4 * h32;  // myq - key + (8 i + j)
+    for (int kb = 0; kb < KB; ++kb) {
+      const int k0 = t * BN + 32 * kb;
+      if (!(wave_live && k0 <= wq_hi && k0 + 31 >= qw0 - W + 1)) continue;
+      const bool full = (k0 + 31 <= qw0) && (k0 >= qw0 + 32 - W);
+      f32x16 si = sinit;
+      if (!full) {
+        // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
+        const int d0 = myq - k0 - 4 * h32;
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
-          float p = fast_exp2(fmaf(sacc[qb][x], c, -lse2[qb]));
-          if (!full) {  // visible iff 0 <= myq - key < W (keys >= T fail it for real rows)
-            const int cst = 8 * (x >> 2) + (x & 3);
-            p = (unsigned)(d0 - cst) < (unsigned)W ? p : 0.f;
-          }
-          dsb[qb][x >> 3][x & 7] = (bf16)(p * (pacc[qb][x] - delta[qb]));
+          const int cst = 8 * (x >> 2) + (x & 3);
+          si[x] = (unsigned)(d0 - cst) < (unsigned)W ? si[x] : -INFINITY;
         }
       }
+      f32x16 sacc = si, pacc = dinit;
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+      for (int s = 0; s < NS; ++s) {
+        sacc = mfma32(frag_operand<D>(kf, kb, s, lane), qreg[s], sacc);
+        pacc = mfma32(frag_operand<D>(vf, kb, s, lane), doreg[s], pacc);
+      }
+      bf16x8 dsb[2];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const bf16x8 ktop = lds_operand_tr(kr + (32 * kb + 16 * kk) * D + 32 * db, D, lane);
+      for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) dqacc[qb][db] = mfma32(ktop, dsb[qb][kk], dqacc[qb][db]);
-        }
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dqacc[db] = mfma32(lds_operand_tr(kr + (32 * kb + 16 * kk) * D + 32 * db, D, lane), dsb[kk], dqacc[db]);
     }
   };
 
-  // Triple-buffered: see attn_fwd.hip.
-  auto stage = [&](int t, const bf16* kf, const bf16* kr, const bf16* vf, bf16* kfn, bf16* krn, bf16* vfn) __attribute__((always_inline)) {
+  // Triple-buffered: before tile t is read each wave waits for its own copy of
+  // tile t (tile t + 1 may still be in flight); the barrier then makes every
+  // copy visible and frees the buffer of tile t - 1, into which tile t + 2 is
+  // issued at once.
+  auto stage = [&](int t, const bf16* kf, const bf16* kr, const bf16* vf, bf16* kfn, bf16* krn, bf16* vfn)
+                   __attribute__((always_inline)) {
     if (t + 1 <= t_hi)
       dma_barrier<PER>();
     else
@@ -173,35 +190,34 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
     stage(t + 2, kf2, kr2, vf2, kf1, kr1, vf1);
   }
 
+  if (myq < T) {
+    bf16* dqrow = a.dq + b * a.sdq[0] + h * a.sdq[2] + (int64_t)myq * a.sdq[1];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int myq = qw0 + 32 * qb + l32;
-    if (myq < T) {
-      bf16* dqrow = a.dq + b * a.sdq[0] + h * a.sdq[2] + (int64_t)myq * a.sdq[1];
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+      for (int i = 0; i < 4; ++i) {
+        bf16x4 v4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bf16x4 v4;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v4[j] = (bf16)(dqacc[qb][db][4 * i + j] * a.scale);
-          *reinterpret_cast<bf16x4*>(dqrow + 32 * db + 8 * i + 4 * h32) = v4;
-        }
-    }
+        for (int j = 0; j < 4; ++j) v4[j] = (bf16)(dqacc[db][4 * i + j] * a.scale);
+        *reinterpret_cast<bf16x4*>(dqrow + 32 * db + 8 * i + 4 * h32) = v4;
+      }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV.  Per wave, lanes own key columns of S = Q K^T and dP = dO V^T (K and
-// V stay in VGPRs as B operands, 64 keys per wave so each LDS operand feeds two
-// MFMAs); lse2 and delta of the query rows come from LDS.  dV^T += dO^T P and
-// dK^T += Q^T dS read dO^T / Q^T transposed from row-major copies.
+// dK, dV.  Per wave, lanes own key columns of S = Q K^T and dP = dO V^T (K, pre-
+// multiplied by scale * log2(e), and V stay in VGPRs as B operands); the start
+// values of the S and dP accumulators, -lse * log2(e) and -delta of the query
+// rows, come from LDS.  dV^T += dO^T P and dK^T += Q^T dS read dO^T / Q^T
+// transposed from row-major copies.
 // ---------------------------------------------------------------------------
-template <int D, int KB, int BMQ, int NBUF>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
-  constexpr int NW = 4, KW = 32 * KB, BNK = NW * KW;
+template <int D, int NBUF>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
+  constexpr int NW = 4, BNK = NW * 32, BMQ = 32;
+  constexpr int NDB = D / 32, NS = D / 16;
   constexpr int TILE = BMQ * D;
-  static_assert(BMQ == 32, "one 32-row query block per tile");
+  static_assert(NBUF == 2 || NBUF == 3, "double or triple buffering");
+  constexpr int TILE3 = NBUF == 3 ? TILE : 8;
   __shared__ __attribute__((aligned(1024))) bf16 qf0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16 qr0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16 df0[TILE];
@@ -210,13 +226,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16 qr1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16 df1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16 dr1[TILE];
-  static_assert(NBUF == 2 || NBUF == 3, "double or triple buffering");
-  constexpr int TILE3 = NBUF == 3 ? TILE : 8;
   __shared__ __attribute__((aligned(1024))) bf16 qf2[TILE3];
   __shared__ __attribute__((aligned(1024))) bf16 qr2[TILE3];
   __shared__ __attribute__((aligned(1024))) bf16 df2[TILE3];
   __shared__ __attribute__((aligned(1024))) bf16 dr2[TILE3];
-  __shared__ __attribute__((aligned(256))) float st0[128];  // [0, 64): lse2, [64, 128): delta
+  __shared__ __attribute__((aligned(256))) float st0[128];  // [0, 64): -lse * log2(e), [64, 128): -delta
   __shared__ __attribute__((aligned(256))) float st1[128];
   __shared__ __attribute__((aligned(256))) float st2[NBUF == 3 ? 128 : 4];
   constexpr int PER = 4 * TILE / 512 / NW;  // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
@@ -231,21 +245,21 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h32 = lane >> 5;
-  const int k0 = kt * BNK, kw0 = k0 + KW * wave;
+  const int k0 = kt * BNK, kw0 = k0 + 32 * wave, mykey = kw0 + l32;
+  const float c = a.scale_log2;
 
-  // K^T / V^T as B operands: lane l of block kb holds k[kw0 + 32 kb + l % 32][16 s + 8 (l / 32) + e].
-  bf16x8 kreg[KB][D / 16], vreg[KB][D / 16];
+  // K^T (times scale * log2(e)) and V^T as B operands: lane l holds row
+  // kw0 + l % 32, columns 16 s + 8 (l / 32) + e.
+  bf16x8 kreg[NS], vreg[NS];
   {
     const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
     const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
     const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        kreg[kb][s] = slab_load(rk, kw0 + 32 * kb + l32, sk2, 16 * s + 8 * h32);
-        vreg[kb][s] = slab_load(rv, kw0 + 32 * kb + l32, sv2, 16 * s + 8 * h32);
-      }
+    for (int s = 0; s < NS; ++s) {
+      kreg[s] = scale_bf16x8(slab_load(rk, mykey, sk2, 16 * s + 8 * h32), c);
+      vreg[s] = slab_load(rv, mykey, sv2, 16 * s + 8 * h32);
+    }
   }
   drain_vmem();
 
@@ -266,8 +280,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
     dma_frags<BMQ, D, NW>(rdo, sdo2, qs, df, wave, lane);
     dma_rows<BMQ, D, NW>(rdo, sdo2, qs, dr, wave, lane);
     if (wave < 2) {
-      // wave 0: lse2 rows qs.., wave 1: delta rows qs.. (fp32, 64 lanes x 4 bytes; rows >= T read 0)
-      const int64_t plane = wave == 0 ? (int64_t)(a.B * H) * T : 0;
+      // wave 0: -lse * log2(e) of rows qs.., wave 1: -delta of rows qs..
+      // (fp32, 64 lanes x 4 bytes; rows >= T read 0)
+      const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;
       const float* base = a.delta + plane + ((int64_t)b * H + hq) * T;
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, T * 4, 0x00020000);
@@ -277,76 +292,69 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
   load_tile(0, qf0, qr0, df0, dr0, st0);
   if (NBUF == 3 && n_iter > 1) load_tile(1, qf1, qr1, df1, dr1, st1);
 
-  f32x16 dkacc[KB][D / 32], dvacc[KB][D / 32];
+  f32x16 dkacc[NDB], dvacc[NDB];
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
-      dkacc[kb][db] = zero16();
-      dvacc[kb][db] = zero16();
-    }
+  for (int db = 0; db < NDB; ++db) {
+    dkacc[db] = zero16();
+    dvacc[db] = zero16();
+  }
 
   const bool wave_live = kw0 < T;
-  const int wk_hi = min(kw0 + KW - 1, T - 1);
-  const float c = a.scale_log2;
+  const int wk_hi = min(kw0 + 31, T - 1);
 
   auto tile_step = [&](const int it, const bf16* qf, const bf16* qr, const bf16* df, const bf16* dr,
                        const float* st) __attribute__((always_inline)) {
     const int qs = (tq_lo + it % nq) * BMQ;
     if (!(wave_live && qs <= wk_hi + W - 1 && qs + BMQ - 1 >= kw0)) return;
-    // Query rows >= T need no mask: their Q, dO, lse2 and delta arrive as zeros,
-    // so they add exactly zero to dK and dV.
-    const bool full = (qs >= kw0 + KW - 1) && (qs + BMQ - 1 - W + 1 <= kw0);
+    // Query rows >= T need no mask: their Q, dO and start values arrive as
+    // zeros, so they add exactly zero to dK and dV.
+    const bool full = (qs >= kw0 + 31) && (qs + BMQ - 1 - kw0 < W);
 
-    f32x16 sacc[KB], pacc[KB];
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      sacc[kb] = zero16();
-      pacc[kb] = zero16();
-    }
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const bf16x8 qop = frag_operand<D>(qf, 0, s, lane);
-      const bf16x8 dop = frag_operand<D>(df, 0, s, lane);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        sacc[kb] = mfma32(qop, kreg[kb][s], sacc[kb]);
-        pacc[kb] = mfma32(dop, vreg[kb][s], pacc[kb]);
-      }
-    }
-    bf16x8 pb[KB][2], dsb[KB][2];
+    // Start values: element x = 4 i + j of the accumulator is query row
+    // qs + 8 i + 4 h32 + j.
+    f32x16 si, di;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r0 = 8 * i + 4 * h32;
-      const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + r0);
-      const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + 64 + r0);
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 8 * i + 4 * h32);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + 64 + 8 * i + 4 * h32);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int d0 = qs + r0 - (kw0 + 32 * kb + l32);  // query - key, for j = 0
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float p = fast_exp2(fmaf(sacc[kb][4 * i + j], c, -l4[j]));
-          if (!full) p = (unsigned)(d0 + j) < (unsigned)W ? p : 0.f;
-          pb[kb][i >> 1][4 * (i & 1) + j] = (bf16)p;
-          dsb[kb][i >> 1][4 * (i & 1) + j] = (bf16)(p * (pacc[kb][4 * i + j] - d4[j]));
-        }
+      for (int j = 0; j < 4; ++j) {
+        si[4 * i + j] = l4[j];
+        di[4 * i + j] = d4[j];
       }
     }
+    if (!full) {
+      const int d0 = qs + 4 * h32 - mykey;  // query - key for x = 0
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+      for (int x = 0; x < 16; ++x) {
+        const int cst = 8 * (x >> 2) + (x & 3);
+        si[x] = (unsigned)(d0 + cst) < (unsigned)W ? si[x] : -INFINITY;
+      }
+    }
+
+    f32x16 sacc = si, pacc = di;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 dtop = lds_operand_tr(dr + 16 * kk * D + 32 * db, D, lane);
-        const bf16x8 qtop = lds_operand_tr(qr + 16 * kk * D + 32 * db, D, lane);
+    for (int s = 0; s < NS; ++s) {
+      sacc = mfma32(frag_operand<D>(qf, 0, s, lane), kreg[s], sacc);
+      pacc = mfma32(frag_operand<D>(df, 0, s, lane), vreg[s], pacc);
+    }
+    bf16x8 pb[2], dsb[2];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          dvacc[kb][db] = mfma32(dtop, pb[kb][kk], dvacc[kb][db]);
-          dkacc[kb][db] = mfma32(qtop, dsb[kb][kk], dkacc[kb][db]);
-        }
+    for (int x = 0; x < 16; ++x) {
+      const float p = fast_exp2(sacc[x]);
+      pb[x >> 3][x & 7] = (bf16)p;
+      dsb[x >> 3][x & 7] = (bf16)(p * pacc[x]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        dvacc[db] = mfma32(lds_operand_tr(dr + 16 * kk * D + 32 * db, D, lane), pb[kk], dvacc[db]);
+        dkacc[db] = mfma32(lds_operand_tr(qr + 16 * kk * D + 32 * db, D, lane), dsb[kk], dkacc[db]);
       }
   };
 
-  // Triple-buffered: see attn_fwd.hip.  Waves 0 and 1 also copy the row
+  // Triple-buffered: see attn_bwd_dq_kernel.  Waves 0 and 1 also copy the row
   // statistics, one more DMA instruction per tile.
   auto stage = [&](int it, const bf16* qf, const bf16* qr, const bf16* df, const bf16* dr, const float* st,
                    bf16* qfn, bf16* qrn, bf16* dfn, bf16* drn, float* stn) __attribute__((always_inline)) {
@@ -377,48 +385,42 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
   }
 
+  if (mykey < T) {
+    bf16* dkrow = a.dk + b * a.sdk[0] + hk * a.sdk[2] + (int64_t)mykey * a.sdk[1];
+    bf16* dvrow = a.dv + b * a.sdv[0] + hk * a.sdv[2] + (int64_t)mykey * a.sdv[1];
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    const int mykey = kw0 + 32 * kb + l32;
-    if (mykey < T) {
-      bf16* dkrow = a.dk + b * a.sdk[0] + hk * a.sdk[2] + (int64_t)mykey * a.sdk[1];
-      bf16* dvrow = a.dv + b * a.sdv[0] + hk * a.sdv[2] + (int64_t)mykey * a.sdv[1];
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+      for (int i = 0; i < 4; ++i) {
+        bf16x4 k4, v4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bf16x4 k4, v4;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            k4[j] = (bf16)(dkacc[kb][db][4 * i + j] * a.scale);
-            v4[j] = (bf16)dvacc[kb][db][4 * i + j];
-          }
-          *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * i + 4 * h32) = k4;
-          *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * i + 4 * h32) = v4;
+        for (int j = 0; j < 4; ++j) {
+          k4[j] = (bf16)(dkacc[db][4 * i + j] * a.scale);
+          v4[j] = (bf16)dvacc[db][4 * i + j];
         }
-    }
+        *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * i + 4 * h32) = k4;
+        *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * i + 4 * h32) = v4;
+      }
   }
 }
 
 template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
-  constexpr int QB = D == 64 ? 2 : 1;
-  constexpr int KB = 2;
   if (phases & kBwdDq) {
-    constexpr int BM = 4 * 32 * QB;
+    constexpr int BM = 4 * 32;
+    constexpr int BN = D == 64 ? 64 : 32;  // three stages: 72 KB of LDS either way
     const int nqt = (a.T + BM - 1) / BM;
     const int64_t blocks = (int64_t)nqt * a.H * a.B;
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, QB>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, BN>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   if (phases & kBwdDkDv) {
-    constexpr int BNK = 4 * 32 * KB;
+    constexpr int BNK = 4 * 32;
     const int nkt = (a.T + BNK - 1) / BNK;
     const int64_t blocks = (int64_t)nkt * a.Hkv * a.B;
-    // D = 128 stays double-buffered: the triple-buffered variant at this register
-    // pressure crashes the ROCm 7.2 compiler (AMDGPU Rewrite AGPR-Copy-MFMA pass).
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, KB, 32, D == 64 ? 3 : 2>), dim3((unsigned)blocks), dim3(kThreads), 0,
+    // D = 128 is double-buffered so that two workgroups share a CU's LDS.
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, D == 64 ? 3 : 2>), dim3((unsigned)blocks), dim3(kThreads), 0,
                        stream, a);
     return hipGetLastError();
   }

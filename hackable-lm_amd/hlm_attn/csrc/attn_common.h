@@ -72,7 +72,7 @@ struct BwdArgs {
   bf16* dq;
   bf16* dk;
   bf16* dv;
-  float* delta;  // 2 x (B, H, T) workspace written by the dq kernel: rowsum(dO * O), then lse * log2(e)
+  float* delta;  // 2 x (B, H, T) workspace written by the dq kernel: -lse * log2(e), then -rowsum(dO * O)
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3];
   int B, T, H, Hkv, W;
   float scale;       // softmax scale

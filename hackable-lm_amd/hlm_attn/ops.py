@@ -107,7 +107,7 @@ def hip_attn_bwd(
     dq = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
     dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     dv = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
-    delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # rowsum(dO*O), lse*log2(e)
+    delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # -lse*log2(e), -rowsum(dO*O)
     with torch.cuda.device(q.device):
         rc = lib.hlm_attn_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),

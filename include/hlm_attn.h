@@ -67,8 +67,8 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 /*
  * Backward: given dO and the forward's o and lse, writes dq, dk, dv (in the
  * layouts given by their strides).  delta_ws is a caller-provided fp32
- * workspace of 2 * B * H * T floats: it receives rowsum(dO * o), then
- * lse * log2(e), each as (B, H, T).  dk/dv are written completely (not
+ * workspace of 2 * B * H * T floats: it receives -lse * log2(e), then
+ * -rowsum(dO * o), each as (B, H, T).  dk/dv are written completely (not
  * accumulated into).
  * Replaces the backward of flash_attn_func (FlashAttention-2's autograd
  * Function, called from /root/reference/kernels.py:841), i.e. the gradient
