@@ -77,9 +77,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 
   const int T = a.T, W = a.W, H = a.H;
   const int nqt = (T + BM - 1) / BM;
-  const int tile = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int qt = nqt - 1 - tile % nqt;
-  const int bh = tile / nqt;
+  // Query tiles with q0 >= W - 1 see a full window: they are ranks 0 .. n_full - 1.
+  const TileId tid_ = tile_order(blockIdx.x, a.B * H, nqt - (W - 1 + BM - 1) / BM);
+  const int qt = nqt - 1 - tid_.rank;  // longest causal rows first
+  const int bh = tid_.unit;
   const int h = bh % H, b = bh / H;
   const int hk = h / (H / a.Hkv);
 
@@ -90,8 +91,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t rq = slab_rsrc(a.q + b * a.sq[0] + h * a.sq[2], a.sq[1], T, D);
   const __amdgpu_buffer_rsrc_t rdo = slab_rsrc(a.dout + b * a.sdo[0] + h * a.sdo[2], a.sdo[1], T, D);
   const __amdgpu_buffer_rsrc_t ro = slab_rsrc(a.o + b * a.so[0] + h * a.so[2], a.so[1], T, D);
-  const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
-  const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
   const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2), so2 = (int)(a.so[1] * 2);
   const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
   const float c = a.scale_log2;
@@ -120,10 +119,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   const int key_lo = max(0, q0 - W + 1);
   const int key_hi = min(T, q0 + BM) - 1;
   const int t_lo = key_lo / BN, t_hi = key_hi / BN;
+  const bf16* kslab = a.k + b * a.sk[0] + hk * a.sk[2];
+  const bf16* vslab = a.v + b * a.sv[0] + hk * a.sv[2];
   auto load_tile = [&](int t, bf16* kf, bf16* kr, bf16* vf) __attribute__((always_inline)) {
-    dma_frags<BN, D, NW>(rk, sk2, t * BN, kf, wave, lane);
-    dma_rows<BN, D, NW>(rk, sk2, t * BN, kr, wave, lane);
-    dma_frags<BN, D, NW>(rv, sv2, t * BN, vf, wave, lane);
+    const __amdgpu_buffer_rsrc_t rkt = slab_rsrc_from(kslab, a.sk[1], T, D, t * BN);
+    const __amdgpu_buffer_rsrc_t rvt = slab_rsrc_from(vslab, a.sv[1], T, D, t * BN);
+    dma_frags<BN, D, NW>(rkt, sk2, 0, kf, wave, lane);
+    dma_rows<BN, D, NW>(rkt, sk2, 0, kr, wave, lane);
+    dma_frags<BN, D, NW>(rvt, sv2, 0, vf, wave, lane);
   };
   load_tile(t_lo, kf0, kr0, vf0);
   if (t_lo + 1 <= t_hi) load_tile(t_lo + 1, kf1, kr1, vf1);
@@ -209,44 +212,84 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 // multiplied by scale * log2(e), and V stay in VGPRs as B operands); the start
 // values of the S and dP accumulators, -lse * log2(e) and -delta of the query
 // rows, come from LDS.  dV^T += dO^T P and dK^T += Q^T dS read dO^T / Q^T
-// transposed from row-major copies.
+// transposed from the same swizzled copies that feed S and dP.
+//
+// Query tiles stream through an NBUF-stage LDS ring, NBUF - 1 tiles ahead of
+// their use, so that the copies of several tiles are in flight while one is
+// computed; the ring slot advances by counting.
 // ---------------------------------------------------------------------------
+template <int PERW, int K>
+__device__ __forceinline__ void dma_barrier_upto(int newer) {
+  if constexpr (K == 0) {
+    dma_barrier<0>();
+  } else {
+    if (newer >= K)
+      dma_barrier<K * PERW>();
+    else
+      dma_barrier_upto<PERW, K - 1>(newer);
+  }
+}
+
 template <int D, int NBUF>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   constexpr int NW = 4, BNK = NW * 32, BMQ = 32;
   constexpr int NDB = D / 32, NS = D / 16;
   constexpr int TILE = BMQ * D;
-  static_assert(NBUF == 2 || NBUF == 3, "double or triple buffering");
-  constexpr int TILE3 = NBUF == 3 ? TILE : 8;
-  __shared__ __attribute__((aligned(1024))) bf16 qf0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 qr0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 df0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 dr0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 qf1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 qr1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 df1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 dr1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 qf2[TILE3];
-  __shared__ __attribute__((aligned(1024))) bf16 qr2[TILE3];
-  __shared__ __attribute__((aligned(1024))) bf16 df2[TILE3];
-  __shared__ __attribute__((aligned(1024))) bf16 dr2[TILE3];
-  __shared__ __attribute__((aligned(256))) float st0[128];  // [0, 64): -lse * log2(e), [64, 128): -delta
-  __shared__ __attribute__((aligned(256))) float st1[128];
-  __shared__ __attribute__((aligned(256))) float st2[NBUF == 3 ? 128 : 4];
-  constexpr int PER = 4 * TILE / 512 / NW;  // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
+  constexpr int PER = 2 * TILE / 512 / NW;  // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
+  static_assert(NBUF >= 3, "at least one tile in flight while one is computed");
+  __shared__ __attribute__((aligned(1024))) bf16 qbuf[NBUF][TILE];
+  __shared__ __attribute__((aligned(1024))) bf16 dbuf[NBUF][TILE];
+  __shared__ __attribute__((aligned(256))) float stbuf[NBUF][128];  // [0, 64): -lse * log2(e), [64, 128): -delta
 
   const int T = a.T, W = a.W, H = a.H, Hkv = a.Hkv;
   const int G = H / Hkv;
   const int nkt = (T + BNK - 1) / BNK;
-  const int tile = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int kt = tile % nkt;  // low key tiles see the most queries: they go first
-  const int bhk = tile / nkt;
+  // Rank-major (measured faster here than the two-phase order): every kv
+  // head's longest key tiles first.
+  const TileId tid_ = rank_major(blockIdx.x, a.B * Hkv);
+  const int kt = tid_.rank;  // low key tiles see the most queries: they go first
+  const int bhk = tid_.unit;
   const int hk = bhk % Hkv, b = bhk / Hkv;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h32 = lane >> 5;
   const int k0 = kt * BNK, kw0 = k0 + 32 * wave, mykey = kw0 + l32;
   const float c = a.scale_log2;
+
+  const int q_lo = k0;
+  const int q_hi = min(T - 1, k0 + BNK - 1 + W - 1);
+  const int tq_lo = q_lo / BMQ, tq_hi = q_hi / BMQ;
+  const int nq = tq_hi - tq_lo + 1;
+  const int n_iter = nq * G;
+  const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2);
+
+  // Tiles are visited head by head (the G query heads of this kv head), query
+  // tile by query tile; the copy pointer (ld_*) runs NBUF - 1 tiles ahead of
+  // the compute pointer.
+  int ld_g = 0, ld_t = 0, ld_slot = 0;
+  auto load_tile = [&]() __attribute__((always_inline)) {
+    const int hq = hk * G + ld_g;
+    const int qs = (tq_lo + ld_t) * BMQ;
+    const __amdgpu_buffer_rsrc_t rq = slab_rsrc_from(a.q + b * a.sq[0] + hq * a.sq[2], a.sq[1], T, D, qs);
+    const __amdgpu_buffer_rsrc_t rdo = slab_rsrc_from(a.dout + b * a.sdo[0] + hq * a.sdo[2], a.sdo[1], T, D, qs);
+    dma_swz<BMQ, D, NW>(rq, sq2, qbuf[ld_slot], wave, lane);
+    dma_swz<BMQ, D, NW>(rdo, sdo2, dbuf[ld_slot], wave, lane);
+    if (wave < 2) {
+      // wave 0: -lse * log2(e) of rows qs.., wave 1: -delta of rows qs..
+      // (fp32, 64 lanes x 4 bytes; rows >= T read 0)
+      const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;
+      const float* base = a.delta + plane + ((int64_t)b * H + hq) * T + qs;
+      const int n = T - qs;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n > 0 ? n * 4 : 0, 0x00020000);
+      lds_dma<4>(rs, stbuf[ld_slot] + 64 * wave, lane * 4);
+    }
+    if (++ld_t == nq) {
+      ld_t = 0;
+      ++ld_g;
+    }
+    if (++ld_slot == NBUF) ld_slot = 0;
+  };
 
   // K^T (times scale * log2(e)) and V^T as B operands: lane l holds row
   // kw0 + l % 32, columns 16 s + 8 (l / 32) + e.
@@ -262,35 +305,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
   }
   drain_vmem();
-
-  const int q_lo = k0;
-  const int q_hi = min(T - 1, k0 + BNK - 1 + W - 1);
-  const int tq_lo = q_lo / BMQ, tq_hi = q_hi / BMQ;
-  const int nq = tq_hi - tq_lo + 1;
-  const int n_iter = nq * G;
-  const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2);
-
-  auto load_tile = [&](int it, bf16* qf, bf16* qr, bf16* df, bf16* dr, float* st) __attribute__((always_inline)) {
-    const int hq = hk * G + it / nq;
-    const int qs = (tq_lo + it % nq) * BMQ;
-    const __amdgpu_buffer_rsrc_t rq = slab_rsrc(a.q + b * a.sq[0] + hq * a.sq[2], a.sq[1], T, D);
-    const __amdgpu_buffer_rsrc_t rdo = slab_rsrc(a.dout + b * a.sdo[0] + hq * a.sdo[2], a.sdo[1], T, D);
-    dma_frags<BMQ, D, NW>(rq, sq2, qs, qf, wave, lane);
-    dma_rows<BMQ, D, NW>(rq, sq2, qs, qr, wave, lane);
-    dma_frags<BMQ, D, NW>(rdo, sdo2, qs, df, wave, lane);
-    dma_rows<BMQ, D, NW>(rdo, sdo2, qs, dr, wave, lane);
-    if (wave < 2) {
-      // wave 0: -lse * log2(e) of rows qs.., wave 1: -delta of rows qs..
-      // (fp32, 64 lanes x 4 bytes; rows >= T read 0)
-      const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;
-      const float* base = a.delta + plane + ((int64_t)b * H + hq) * T;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, T * 4, 0x00020000);
-      lds_dma<4>(rs, st + 64 * wave, (qs + lane) * 4);
-    }
-  };
-  load_tile(0, qf0, qr0, df0, dr0, st0);
-  if (NBUF == 3 && n_iter > 1) load_tile(1, qf1, qr1, df1, dr1, st1);
+  for (int i = 0; i < NBUF - 1 && i < n_iter; ++i) load_tile();
 
   f32x16 dkacc[NDB], dvacc[NDB];
 #pragma unroll
@@ -301,11 +316,26 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
   const bool wave_live = kw0 < T;
   const int wk_hi = min(kw0 + 31, T - 1);
+  int cp_t = 0, cp_slot = 0;  // query tile (within the current head) and ring slot of the compute pointer
 
-  auto tile_step = [&](const int it, const bf16* qf, const bf16* qr, const bf16* df, const bf16* dr,
-                       const float* st) __attribute__((always_inline)) {
-    const int qs = (tq_lo + it % nq) * BMQ;
-    if (!(wave_live && qs <= wk_hi + W - 1 && qs + BMQ - 1 >= kw0)) return;
+  for (int it = 0; it < n_iter; ++it) {
+    // Wait for this wave's copies of tile it (the newer tiles may stay in
+    // flight); the barrier makes every wave's copies visible and frees the
+    // slot of tile it - 1, which takes tile it + NBUF - 1.
+    const int newer = min(NBUF - 2, n_iter - 1 - it);
+    if (wave < 2)
+      dma_barrier_upto<PER + 1, NBUF - 2>(newer);
+    else
+      dma_barrier_upto<PER, NBUF - 2>(newer);
+    if (it + NBUF - 1 < n_iter) load_tile();
+
+    const bf16* qs_t = qbuf[cp_slot];
+    const bf16* ds_t = dbuf[cp_slot];
+    const float* st = stbuf[cp_slot];
+    const int qs = (tq_lo + cp_t) * BMQ;
+    if (++cp_t == nq) cp_t = 0;
+    if (++cp_slot == NBUF) cp_slot = 0;
+    if (!(wave_live && qs <= wk_hi + W - 1 && qs + BMQ - 1 >= kw0)) continue;
     // Query rows >= T need no mask: their Q, dO and start values arrive as
     // zeros, so they add exactly zero to dK and dV.
     const bool full = (qs >= kw0 + 31) && (qs + BMQ - 1 - kw0 < W);
@@ -335,8 +365,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     f32x16 sacc = si, pacc = di;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      sacc = mfma32(frag_operand<D>(qf, 0, s, lane), kreg[s], sacc);
-      pacc = mfma32(frag_operand<D>(df, 0, s, lane), vreg[s], pacc);
+      sacc = mfma32(swz_operand<D>(qs_t, 0, s, lane), kreg[s], sacc);
+      pacc = mfma32(swz_operand<D>(ds_t, 0, s, lane), vreg[s], pacc);
     }
     bf16x8 pb[2], dsb[2];
 #pragma unroll
@@ -349,40 +379,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        dvacc[db] = mfma32(lds_operand_tr(dr + 16 * kk * D + 32 * db, D, lane), pb[kk], dvacc[db]);
-        dkacc[db] = mfma32(lds_operand_tr(qr + 16 * kk * D + 32 * db, D, lane), dsb[kk], dkacc[db]);
+        dvacc[db] = mfma32(swz_operand_tr<D>(ds_t, 16 * kk, 32 * db, lane), pb[kk], dvacc[db]);
+        dkacc[db] = mfma32(swz_operand_tr<D>(qs_t, 16 * kk, 32 * db, lane), dsb[kk], dkacc[db]);
       }
-  };
-
-  // Triple-buffered: see attn_bwd_dq_kernel.  Waves 0 and 1 also copy the row
-  // statistics, one more DMA instruction per tile.
-  auto stage = [&](int it, const bf16* qf, const bf16* qr, const bf16* df, const bf16* dr, const float* st,
-                   bf16* qfn, bf16* qrn, bf16* dfn, bf16* drn, float* stn) __attribute__((always_inline)) {
-    if (NBUF == 3 && it + 1 < n_iter) {
-      if (wave < 2)
-        dma_barrier<PER + 1>();
-      else
-        dma_barrier<PER>();
-    } else {
-      dma_barrier<0>();
-    }
-    if (it + NBUF - 1 < n_iter) load_tile(it + NBUF - 1, qfn, qrn, dfn, drn, stn);
-    tile_step(it, qf, qr, df, dr, st);
-  };
-  if constexpr (NBUF == 3) {
-    for (int it = 0; it < n_iter; it += 3) {
-      stage(it, qf0, qr0, df0, dr0, st0, qf2, qr2, df2, dr2, st2);
-      if (it + 1 >= n_iter) break;
-      stage(it + 1, qf1, qr1, df1, dr1, st1, qf0, qr0, df0, dr0, st0);
-      if (it + 2 >= n_iter) break;
-      stage(it + 2, qf2, qr2, df2, dr2, st2, qf1, qr1, df1, dr1, st1);
-    }
-  } else {
-    for (int it = 0; it < n_iter; it += 2) {
-      stage(it, qf0, qr0, df0, dr0, st0, qf1, qr1, df1, dr1, st1);
-      if (it + 1 >= n_iter) break;
-      stage(it + 1, qf1, qr1, df1, dr1, st1, qf0, qr0, df0, dr0, st0);
-    }
   }
 
   if (mykey < T) {
@@ -408,7 +407,7 @@ template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
   if (phases & kBwdDq) {
     constexpr int BM = 4 * 32;
-    constexpr int BN = D == 64 ? 64 : 32;  // three stages: 72 KB of LDS either way
+    constexpr int BN = 32;  // three stages of 32-key K, K^T and V tiles: 36 KB (D = 64) or 72 KB of LDS
     const int nqt = (a.T + BM - 1) / BM;
     const int64_t blocks = (int64_t)nqt * a.H * a.B;
     hipLaunchKernelGGL((attn_bwd_dq_kernel<D, BN>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
@@ -419,8 +418,9 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
     constexpr int BNK = 4 * 32;
     const int nkt = (a.T + BNK - 1) / BNK;
     const int64_t blocks = (int64_t)nkt * a.Hkv * a.B;
-    // D = 128 is double-buffered so that two workgroups share a CU's LDS.
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, D == 64 ? 3 : 2>), dim3((unsigned)blocks), dim3(kThreads), 0,
+    // Six stages (51 KB) for D = 64, four (66 KB) for D = 128: two or three
+    // workgroups per CU either way.
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, D == 64 ? 6 : 4>), dim3((unsigned)blocks), dim3(kThreads), 0,
                        stream, a);
     return hipGetLastError();
   }

@@ -99,13 +99,29 @@ __device__ __forceinline__ bf16x8 zero_bf16x8() {
   return z;
 }
 
-// Maps a linear workgroup id onto a tile index so that the workgroups that the
-// hardware places on one XCD (ids congruent mod 8) get a contiguous range of
-// tiles.  Neighbouring tiles of one (batch, head) then share that XCD's L2.
-__device__ __forceinline__ int xcd_swizzle(int id, int n) {
-  const int xcd = id & 7, slot = id >> 3;
-  const int per = n >> 3, extra = n & 7;
-  return xcd * per + min(xcd, extra) + slot;
+// Workgroup order.  The grid is rank-major: workgroup id = rank * n_units +
+// unit, where a unit is one (batch, head) slab and rank 0 is the unit's
+// longest tile.  The hardware dispatches ids in increasing order, so the
+// longest tiles start first and the short ones fill the tail; and it places
+// id on XCD id % 8, so when n_units is a multiple of 8 every tile of a unit
+// runs on the same XCD and its neighbouring tiles share that XCD's L2.
+struct TileId {
+  int rank, unit;
+};
+__device__ __forceinline__ TileId rank_major(int id, int n_units) { return {id / n_units, id % n_units}; }
+
+// Two-phase order for grids of n_units * n_ranks workgroups where ranks
+// 0 .. n_full - 1 all have the unit's full length: each XCD (ids congruent
+// mod 8) owns the units congruent to it mod 8 and first runs their
+// full-length tiles unit by unit (a unit's neighbouring tiles share L2 while
+// they run), then the shorter ranks, longest first, so the short tiles fill
+// the tail.  Falls back to rank_major when n_units is not a multiple of 8.
+__device__ __forceinline__ TileId tile_order(int id, int n_units, int n_full) {
+  if ((n_units & 7) != 0 || n_full <= 0) return rank_major(id, n_units);
+  const int xcd = id & 7, slot = id >> 3, per = n_units >> 3;
+  if (slot < per * n_full) return {slot % n_full, 8 * (slot / n_full) + xcd};
+  const int s2 = slot - per * n_full;
+  return {n_full + s2 / per, 8 * (s2 % per) + xcd};
 }
 
 // A/B operand whose 8 contraction values sit contiguously in one LDS row:
@@ -146,6 +162,16 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16* base, int64_t st, int T, int D) {
   const int64_t extent = (int64_t)(T - 1) * st * 2 + 2 * D;  // bytes; < 2^31 (checked by the host)
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
+}
+
+// The same slab seen from row r0 on: rows r0 .. T - 1 of the slab are rows
+// 0 .. T - 1 - r0 of the resource and everything past them (and any r0 >= T)
+// reads as zeros.  Tile copies use this so that their per-lane offsets do not
+// depend on the tile.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc_from(const bf16* base, int64_t st, int T, int D, int r0) {
+  const int64_t extent = (int64_t)(T - 1 - r0) * st * 2 + 2 * D;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)r0 * st), (short)0, extent > 0 ? (int)extent : 0,
+                                           0x00020000);
 }
 
 // 16 bytes of one row at element column `col` through a slab resource.
@@ -204,6 +230,67 @@ __device__ __forceinline__ void dma_frags(__amdgpu_buffer_rsrc_t rs, int st2, in
     const int col = 16 * (j % SPR) + 8 * (lane >> 5);
     lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
   }
+}
+
+// Swizzled fragment layout: one LDS copy of a ROWS x D tile that serves both
+// operand orientations without bank conflicts.  Piece f = rb * (D / 16) + s
+// (1 KB) holds rows 32 rb .. 32 rb + 31, columns 16 s .. 16 s + 15, as 64
+// chunks of 16 bytes; chunk p holds half h = p / 32 (columns 16 s + 8 h ..
+// + 7) of row 32 rb + ((p % 32) ^ 4 h).
+//  * An MFMA operand along the rows (lane l: row l % 32, half l / 32) is one
+//    ds_read_b128 per lane; each group of 16 lanes covers 16 distinct chunk
+//    slots mod 256 bytes.
+//  * A transposed operand (ds_read_b64_tr_b16, 4 rows x both halves per
+//    16-lane group) touches 8 chunks whose slots differ mod 256 bytes, because
+//    the XOR moves the second half of rows 4 m .. 4 m + 3 by 4 slots.
+__device__ __forceinline__ int swz_chunk(int row, int h) { return 32 * h + ((row & 31) ^ (4 * h)); }
+
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ void dma_swz(__amdgpu_buffer_rsrc_t rs, int st2, bf16* lds, int wave, int lane) {
+  constexpr int NI = ROWS * D / 512, SPR = D / 16;  // 1 KB pieces; pieces per 32-row block
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
+  const int h = lane >> 5, r = (lane & 31) ^ (4 * h);
+#pragma unroll
+  for (int i = 0; i < NI / NW; ++i) {
+    const int j = wave + NW * i;
+    const int row = 32 * (j / SPR) + r;
+    const int col = 16 * (j % SPR) + 8 * h;
+    lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
+  }
+}
+
+// Operand (rb, s) along the rows of a swizzled tile: lane l gets row
+// 32 rb + l % 32, columns 16 s + 8 (l / 32) .. + 7.
+template <int D>
+__device__ __forceinline__ bf16x8 swz_operand(const bf16* lds, int rb, int s, int lane) {
+  const int h = lane >> 5;
+  return *reinterpret_cast<const bf16x8*>(lds + (rb * (D / 16) + s) * 512 + swz_chunk(lane & 31, h) * 8);
+}
+
+// Transposed operand of a swizzled tile, contracting over 16 rows r0 ..
+// r0 + 15 (r0 a multiple of 16) for the 32 columns c0 .. c0 + 31 (c0 a
+// multiple of 32): the same values and order as lds_operand_tr on a
+// row-major copy.
+template <int D>
+__device__ __forceinline__ bf16x8 swz_operand_tr(const bf16* lds, int r0, int c0, int lane) {
+  const int g = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
+  const int row = r0 + 4 * (g >> 1) + r;
+  const int s = c0 / 16 + (g & 1), h = c >> 1;
+  const bf16* base = lds + ((row >> 5) * (D / 16) + s) * 512 + 4 * (c & 1);
+  const bf16* p0 = base + swz_chunk(row, h) * 8;
+  const bf16* p1 = base + swz_chunk(row + 8, h) * 8;
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
+  bf16x8 out;
+  const bf16x4 lo_b = __builtin_bit_cast(bf16x4, lo);
+  const bf16x4 hi_b = __builtin_bit_cast(bf16x4, hi);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    out[e] = lo_b[e];
+    out[4 + e] = hi_b[e];
+  }
+  return out;
 }
 
 // Barrier for tiles that arrive by LDS DMA: wait until at most `pending` of

@@ -52,9 +52,10 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
 
   const int T = a.T, W = a.W, H = a.H;
   const int nqt = (T + BM - 1) / BM;
-  const int tile = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int qt = nqt - 1 - tile % nqt;  // longest causal rows first within a head
-  const int bh = tile / nqt;
+  // Query tiles with q0 >= W - 1 see a full window: they are ranks 0 .. n_full - 1.
+  const TileId tid_ = tile_order(blockIdx.x, a.B * H, nqt - (W - 1 + BM - 1) / BM);
+  const int qt = nqt - 1 - tid_.rank;  // longest causal rows first
+  const int bh = tid_.unit;
   const int h = bh % H, b = bh / H;
   const int hk = h / (H / a.Hkv);
 
