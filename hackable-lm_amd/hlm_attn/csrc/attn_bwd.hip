@@ -134,7 +134,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   f32x16 dqacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dqacc[db] = zero16();
-  const f32x16 sinit = splat16(nlse2), dinit = splat16(ndelta);
+  // The start values are kept live (not re-splatted per block) and feed the
+  // first MFMA of each chain as its C operand; masked blocks use a masked copy.
+  f32x16 sinit = splat16(nlse2), dinit = splat16(ndelta);
+  asm volatile("" : "+v"(sinit), "+v"(dinit));
 
   const bool wave_live = qw0 < T;
   const int wq_hi = min(qw0 + 31, T - 1);
@@ -144,31 +147,35 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
     for (int kb = 0; kb < KB; ++kb) {
       const int k0 = t * BN + 32 * kb;
       if (!(wave_live && k0 <= wq_hi && k0 + 31 >= qw0 - W + 1)) continue;
-      const bool full = (k0 + 31 <= qw0) && (k0 >= qw0 + 32 - W);
-      f32x16 si = sinit;
-      if (!full) {
+      auto body = [&](const f32x16& si) __attribute__((always_inline)) {
+        f32x16 sacc = si, pacc = dinit;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          sacc = mfma32(frag_operand<D>(kf, kb, s, lane), qreg[s], sacc);
+          pacc = mfma32(frag_operand<D>(vf, kb, s, lane), doreg[s], pacc);
+        }
+        bf16x8 dsb[2];
+#pragma unroll
+        for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            dqacc[db] = mfma32(lds_operand_tr(kr + (32 * kb + 16 * kk) * D + 32 * db, D, lane), dsb[kk], dqacc[db]);
+      };
+      if ((k0 + 31 <= qw0) && (k0 >= qw0 + 32 - W)) {
+        body(sinit);
+      } else {
         // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
+        f32x16 si = sinit;
         const int d0 = myq - k0 - 4 * h32;
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
           const int cst = 8 * (x >> 2) + (x & 3);
           si[x] = (unsigned)(d0 - cst) < (unsigned)W ? si[x] : -INFINITY;
         }
+        body(si);
       }
-      f32x16 sacc = si, pacc = dinit;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        sacc = mfma32(frag_operand<D>(kf, kb, s, lane), qreg[s], sacc);
-        pacc = mfma32(frag_operand<D>(vf, kb, s, lane), doreg[s], pacc);
-      }
-      bf16x8 dsb[2];
-#pragma unroll
-      for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          dqacc[db] = mfma32(lds_operand_tr(kr + (32 * kb + 16 * kk) * D + 32 * db, D, lane), dsb[kk], dqacc[db]);
     }
   };
 
@@ -265,30 +272,36 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
   // Tiles are visited head by head (the G query heads of this kv head), query
   // tile by query tile; the copy pointer (ld_*) runs NBUF - 1 tiles ahead of
-  // the compute pointer.
+  // the compute pointer.  Its buffer resources walk down the slabs by one
+  // tile per copy.
   int ld_g = 0, ld_t = 0, ld_slot = 0;
+  const int64_t qstep = (int64_t)BMQ * a.sq[1] * 2, dostep = (int64_t)BMQ * a.sdo[1] * 2;
+  const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;  // waves 0 / 1 copy -lse*log2(e) / -delta
+  SlabCursor cq, cdo, cst;
+  auto start_head = [&]() __attribute__((always_inline)) {
+    const int hq = hk * G + ld_g, qs = tq_lo * BMQ;
+    cq = slab_cursor(a.q + b * a.sq[0] + hq * a.sq[2], a.sq[1], T, D, qs);
+    cdo = slab_cursor(a.dout + b * a.sdo[0] + hq * a.sdo[2], a.sdo[1], T, D, qs);
+    cst = {(uint64_t)(uintptr_t)(a.delta + plane + ((int64_t)b * H + hq) * T + qs), (int64_t)(T - qs) * 4};
+  };
+  start_head();
+  const SwzOffsets<BMQ, D, NW> oq = swz_offsets<BMQ, D, NW>(sq2, wave, lane);
+  const SwzOffsets<BMQ, D, NW> odo = swz_offsets<BMQ, D, NW>(sdo2, wave, lane);
+  const unsigned lq = lds_addr(qbuf), ldo = lds_addr(dbuf), lst = lds_addr(stbuf) + 256 * wave;
   auto load_tile = [&]() __attribute__((always_inline)) {
-    const int hq = hk * G + ld_g;
-    const int qs = (tq_lo + ld_t) * BMQ;
-    const __amdgpu_buffer_rsrc_t rq = slab_rsrc_from(a.q + b * a.sq[0] + hq * a.sq[2], a.sq[1], T, D, qs);
-    const __amdgpu_buffer_rsrc_t rdo = slab_rsrc_from(a.dout + b * a.sdo[0] + hq * a.sdo[2], a.sdo[1], T, D, qs);
-    dma_swz<BMQ, D, NW>(rq, sq2, qbuf[ld_slot], wave, lane);
-    dma_swz<BMQ, D, NW>(rdo, sdo2, dbuf[ld_slot], wave, lane);
-    if (wave < 2) {
-      // wave 0: -lse * log2(e) of rows qs.., wave 1: -delta of rows qs..
-      // (fp32, 64 lanes x 4 bytes; rows >= T read 0)
-      const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;
-      const float* base = a.delta + plane + ((int64_t)b * H + hq) * T + qs;
-      const int n = T - qs;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n > 0 ? n * 4 : 0, 0x00020000);
-      lds_dma<4>(rs, stbuf[ld_slot] + 64 * wave, lane * 4);
-    }
+    dma_swz_at<BMQ, D, NW>(cq.rsrc(), oq, lq + ld_slot * (TILE * 2), wave);
+    dma_swz_at<BMQ, D, NW>(cdo.rsrc(), odo, ldo + ld_slot * (TILE * 2), wave);
+    if (wave < 2) lds_dma_at<4>(cst.rsrc(), lst + ld_slot * 512, lane * 4);  // fp32 rows, 64 lanes x 4 bytes
+    if (++ld_slot == NBUF) ld_slot = 0;
     if (++ld_t == nq) {
       ld_t = 0;
       ++ld_g;
+      if (ld_g < G) start_head();
+    } else {
+      cq.advance(qstep);
+      cdo.advance(dostep);
+      cst.advance(BMQ * 4);
     }
-    if (++ld_slot == NBUF) ld_slot = 0;
   };
 
   // K^T (times scale * log2(e)) and V^T as B operands: lane l holds row

@@ -197,6 +197,44 @@ __device__ __forceinline__ void lds_dma(__amdgpu_buffer_rsrc_t rs, const void* l
     asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
 }
 
+// LDS byte address of a __shared__ location (taken once per kernel; the
+// per-tile addresses are then plain 32-bit offsets from it, so the loops carry
+// no generic-to-LDS pointer conversions).
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void*)p);
+}
+
+// As lds_dma, to an LDS byte address.
+template <int bytes>
+__device__ __forceinline__ void lds_dma_at(__amdgpu_buffer_rsrc_t rs, unsigned ldsaddr, int voff) {
+  if constexpr (bytes == 16)
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
+  else
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
+}
+
+// A buffer resource that walks down a slab tile by tile: `addr` is the byte
+// address of the current tile's first row and `bytes` the bytes left in the
+// slab from there (<= 0 past the end: every read returns zeros).
+struct SlabCursor {
+  uint64_t addr;
+  int64_t bytes;
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
+    const int n = bytes > 0 ? (int)bytes : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, n, 0x00020000);
+  }
+  __device__ __forceinline__ void advance(int64_t step) {
+    addr += step;
+    bytes -= step;
+  }
+};
+
+// Cursor over a (batch, head) slab of T rows of 2*D bytes at row stride st
+// elements, positioned at row r0.
+__device__ __forceinline__ SlabCursor slab_cursor(const bf16* base, int64_t st, int T, int D, int r0) {
+  return {(uint64_t)(uintptr_t)(base + (int64_t)r0 * st), (int64_t)(T - 1 - r0) * st * 2 + 2 * D};
+}
+
 // Direct buffer -> LDS copies of a ROWS x D tile starting at row r0 (st2 = row
 // stride in bytes).  Each instruction moves 1 KB, and a layout is chosen by
 // choosing each lane's source address.  The NW waves of a workgroup split the
@@ -257,6 +295,33 @@ __device__ __forceinline__ void dma_swz(__amdgpu_buffer_rsrc_t rs, int st2, bf16
     const int col = 16 * (j % SPR) + 8 * h;
     lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
   }
+}
+
+// dma_swz to the LDS byte address `lds` with the per-lane source offsets
+// precomputed by swz_offsets (they depend only on the lane and the row stride).
+template <int ROWS, int D, int NW>
+struct SwzOffsets {
+  int v[ROWS * D / 512 / NW];
+};
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ SwzOffsets<ROWS, D, NW> swz_offsets(int st2, int wave, int lane) {
+  constexpr int NI = ROWS * D / 512, SPR = D / 16;
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
+  SwzOffsets<ROWS, D, NW> o;
+  const int h = lane >> 5, r = (lane & 31) ^ (4 * h);
+#pragma unroll
+  for (int i = 0; i < NI / NW; ++i) {
+    const int j = wave + NW * i;
+    o.v[i] = (32 * (j / SPR) + r) * st2 + (16 * (j % SPR) + 8 * h) * 2;
+  }
+  return o;
+}
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ void dma_swz_at(__amdgpu_buffer_rsrc_t rs, const SwzOffsets<ROWS, D, NW>& o, unsigned lds,
+                                           int wave) {
+  constexpr int NI = ROWS * D / 512;
+#pragma unroll
+  for (int i = 0; i < NI / NW; ++i) lds_dma_at<16>(rs, lds + (wave + NW * i) * 1024, o.v[i]);
 }
 
 // Operand (rb, s) along the rows of a swizzled tile: lane l gets row
