@@ -54,30 +54,39 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ (+ the workspace).  Same orientation as the forward: per wave, lanes own
-// query columns of S^T = K Q^T and dP^T = V dO^T, so -lse * log2(e) and
-// -delta are per-lane constants (splat start values of the accumulators);
-// dQ^T += K^T dS^T reads K^T transposed from the row-major copy of the K tile.
+// dQ (+ the workspace).  Every global access is coalesced.
+//  * K/V tiles of 32 keys stream through an NBUF-slot LDS ring in the cs
+//    layout (one 1 KB DMA instruction = whole rows); each tile serves the S
+//    operand (rows) and the K^T operand of dQ (transposed) from one copy.
+//  * Each wave's own Q and dO rows arrive by DMA in the cs layout in ring slots
+//    that the ring does not use yet (PRE tiles are already in flight in the
+//    first slots), and are read from there into operand registers.
+//  * O is read with coalesced loads (whole rows per instruction) only to form
+//    delta = rowsum(dO * O) together with the staged dO.
+//  * dQ leaves through LDS: each wave writes its 32 x D block into a cs tile
+//    and stores whole rows.
+// Every vector-memory load is inline asm with explicit waits (the compiler
+// tracks none of them) and no store is issued before the loop ends, so inside
+// the loop the vector-memory counter counts tile copies only.
 // ---------------------------------------------------------------------------
-template <int D, int BN>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
-  constexpr int NW = 4, BM = NW * 32;
-  constexpr int KB = BN / 32, NDB = D / 32, NS = D / 16;
-  constexpr int TILE = BN * D;
-  constexpr int PER = 3 * TILE / 512 / NW;  // DMA instructions per wave per tile
-  __shared__ __attribute__((aligned(1024))) bf16 kf0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 kr0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 vf0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 kf1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 kr1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 vf1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 kf2[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 kr2[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 vf2[TILE];
+template <int D, int NBUF, int PRE>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
+  using L = CS<D>;
+  constexpr int NW = 4, BM = NW * 32, BN = 32;
+  constexpr int NDB = D / 32, NS = D / 16;
+  constexpr int TILEB = BN * D * 2;       // bytes of one K or V tile
+  constexpr int SLOTB = 2 * TILEB;        // one ring slot: K and V
+  constexpr int CPT = TILEB / 1024;       // 1 KB chunks per tile
+  constexpr int PER = 2 * CPT / NW;       // DMA instructions per wave per tile
+  constexpr int NCH = 32 / L::RPC;        // chunks of a wave's 32 rows
+  constexpr int WSTG = 2 * NCH * 1024;    // staging bytes per wave (Q and dO)
+  static_assert(CPT % NW == 0, "tile chunks split evenly over the waves");
+  static_assert(PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
+  static_assert(NBUF * PER < 64 && 2 * NCH + PRE * PER < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
 
   const int T = a.T, W = a.W, H = a.H;
   const int nqt = (T + BM - 1) / BM;
-  // Query tiles with q0 >= W - 1 see a full window: they are ranks 0 .. n_full - 1.
   const TileId tid_ = tile_order(blockIdx.x, a.B * H, nqt - (W - 1 + BM - 1) / BM);
   const int qt = nqt - 1 - tid_.rank;  // longest causal rows first
   const int bh = tid_.unit;
@@ -91,126 +100,167 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t rq = slab_rsrc(a.q + b * a.sq[0] + h * a.sq[2], a.sq[1], T, D);
   const __amdgpu_buffer_rsrc_t rdo = slab_rsrc(a.dout + b * a.sdo[0] + h * a.sdo[2], a.sdo[1], T, D);
   const __amdgpu_buffer_rsrc_t ro = slab_rsrc(a.o + b * a.so[0] + h * a.so[2], a.so[1], T, D);
+  const __amdgpu_buffer_rsrc_t rl = row_rsrc(a.lse + (int64_t)bh * T, T);
+  const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
+  const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
   const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2), so2 = (int)(a.so[1] * 2);
   const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
   const float c = a.scale_log2;
 
-  // Q^T (times scale * log2(e)) and dO^T as B operands: lane l holds row
-  // qw0 + l % 32, columns 16 s + 8 (l / 32) + e.  Rows >= T read as zeros.
-  bf16x8 qreg[NS], doreg[NS];
-  float dpart = 0.f;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int col = 16 * s + 8 * h32;
-    qreg[s] = scale_bf16x8(slab_load(rq, myq, sq2, col), c);
-    doreg[s] = slab_load(rdo, myq, sdo2, col);
-    const bf16x8 o8 = slab_load(ro, myq, so2, col);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dpart += (float)doreg[s][e] * (float)o8[e];
-  }
-  const float ndelta = -(dpart + __shfl_xor(dpart, 32));
-  const float nlse2 = myq < T ? -a.lse[(int64_t)bh * T + myq] * kLog2e : 0.f;
-  if (myq < T && h32 == 0) {
-    a.delta[(int64_t)bh * T + myq] = nlse2;
-    a.delta[(int64_t)(a.B * H + bh) * T + myq] = ndelta;
-  }
-  drain_vmem();
+  const unsigned lring = lds_addr(ring);
+  const unsigned stg_q = lring + PRE * SLOTB + wave * WSTG, stg_do = stg_q + NCH * 1024;
 
+  // 1. The wave's O rows (coalesced: chunk k = rows qw0 + RPC k + l / U) and lse.
+  bf16x8 oc[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+    oc[k] = asm_load_b128(ro, (qw0 + L::dma_row(k, lane)) * so2 + (lane % L::U) * 16);
+  float lraw = asm_load_b32(rl, myq * 4);  // 0 for rows >= T
+  // 2. Its Q and dO rows into the staging area (cs layout).
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int row = qw0 + L::dma_row(k, lane), cb = L::dma_col_bytes(k, lane);
+    lds_dma_at<16>(rq, stg_q + k * 1024, row * sq2 + cb);
+    lds_dma_at<16>(rdo, stg_do + k * 1024, row * sdo2 + cb);
+  }
+  // 3. The first ring tiles.
   const int key_lo = max(0, q0 - W + 1);
   const int key_hi = min(T, q0 + BM) - 1;
-  const int t_lo = key_lo / BN, t_hi = key_hi / BN;
-  const bf16* kslab = a.k + b * a.sk[0] + hk * a.sk[2];
-  const bf16* vslab = a.v + b * a.sv[0] + hk * a.sv[2];
-  auto load_tile = [&](int t, bf16* kf, bf16* kr, bf16* vf) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rkt = slab_rsrc_from(kslab, a.sk[1], T, D, t * BN);
-    const __amdgpu_buffer_rsrc_t rvt = slab_rsrc_from(vslab, a.sv[1], T, D, t * BN);
-    dma_frags<BN, D, NW>(rkt, sk2, 0, kf, wave, lane);
-    dma_rows<BN, D, NW>(rkt, sk2, 0, kr, wave, lane);
-    dma_frags<BN, D, NW>(rvt, sv2, 0, vf, wave, lane);
+  const int t_lo = key_lo / BN, n_tiles = key_hi / BN - t_lo + 1;
+  int kof[CPT / NW], vof[CPT / NW];
+#pragma unroll
+  for (int i = 0; i < CPT / NW; ++i) {
+    const int j = wave + NW * i;
+    kof[i] = L::dma_row(j, lane) * sk2 + L::dma_col_bytes(j, lane);
+    vof[i] = L::dma_row(j, lane) * sv2 + L::dma_col_bytes(j, lane);
+  }
+  auto load_tile = [&](int t) __attribute__((always_inline)) {
+    const unsigned slot = lring + (unsigned)(t % NBUF) * SLOTB;
+    const int kb = (t_lo + t) * BN * sk2, vb = (t_lo + t) * BN * sv2;
+#pragma unroll
+    for (int i = 0; i < CPT / NW; ++i) {
+      const unsigned piece = (unsigned)(wave + NW * i) * 1024;
+      lds_dma_at<16>(rk, slot + piece, kb + kof[i]);
+      lds_dma_at<16>(rv, slot + TILEB + piece, vb + vof[i]);
+    }
   };
-  load_tile(t_lo, kf0, kr0, vf0);
-  if (t_lo + 1 <= t_hi) load_tile(t_lo + 1, kf1, kr1, vf1);
+  const int n_pre = min(PRE, n_tiles);
+  for (int t = 0; t < n_pre; ++t) load_tile(t);
+
+  // 4. Wait for this wave's rows (the first tiles may still be in flight).
+  vm_wait_upto<PER, PRE>(n_pre);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) touch(oc[k]);
+  touch(lraw);
+
+  int off_s[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) off_s[s] = L::byte(l32, 2 * s + h32);
+  int tro[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tro[db][0] = cs_tr_off<D>(db, 0, lane);
+    tro[db][1] = cs_tr_off<D>(db, 1, lane);
+  }
+
+  // Q^T (times scale * log2(e)) and dO^T as B operands: lane l holds row
+  // qw0 + l % 32, columns 16 s + 8 (l / 32) + e.
+  bf16x8 qreg[NS], doreg[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    qreg[s] = scale_bf16x8(cs_operand<D>(stg_q, off_s[s], 0), c);
+    doreg[s] = cs_operand<D>(stg_do, off_s[s], 0);
+  }
+  // delta of row RPC k + l / U: the U lanes of a row hold its 16-byte pieces.
+  float dpart[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const bf16x8 d8 = lds_read_b128(stg_do + L::byte(L::dma_row(k, lane), lane % L::U));
+    float p = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p += (float)oc[k][e] * (float)d8[e];
+#pragma unroll
+    for (int m = 1; m < L::U; m <<= 1) p += __shfl_xor(p, m);
+    dpart[k] = p;
+  }
+  float dsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const float t = __shfl(dpart[k], L::U * (l32 % L::RPC));
+    dsum = (l32 / L::RPC == k) ? t : dsum;
+  }
+  const float ndelta = -dsum;
+  const float nlse2 = -lraw * kLog2e;
 
   f32x16 dqacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dqacc[db] = zero16();
-  // The start values are kept live (not re-splatted per block) and feed the
-  // first MFMA of each chain as its C operand; masked blocks use a masked copy.
-  f32x16 sinit = splat16(nlse2), dinit = splat16(ndelta);
-  asm volatile("" : "+v"(sinit), "+v"(dinit));
 
   const bool wave_live = qw0 < T;
   const int wq_hi = min(qw0 + 31, T - 1);
 
-  auto tile_step = [&](const int t, const bf16* kf, const bf16* kr, const bf16* vf) __attribute__((always_inline)) {
+  int issued_hi = n_pre - 1;
+  for (int it = 0; it < n_tiles; ++it) {
+    // Wait for this wave's copies of tile it (newer tiles may stay in flight);
+    // the barrier makes every wave's copies visible and frees the slot of tile
+    // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
+    // NBUF - 1 tiles ahead.
+    dma_barrier_upto<PER, NBUF - 1>(issued_hi - it);
+    const int want = min(it + NBUF - 1, n_tiles - 1);
+    while (issued_hi < want) load_tile(++issued_hi);
+
+    const unsigned kt = lring + (unsigned)(it % NBUF) * SLOTB, vt = kt + TILEB;
+    const int k0 = (t_lo + it) * BN;
+    if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
+    const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
+    f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
+    if (!full) {
+      // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
+      const int d0 = myq - k0 - 4 * h32;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int k0 = t * BN + 32 * kb;
-      if (!(wave_live && k0 <= wq_hi && k0 + 31 >= qw0 - W + 1)) continue;
-      auto body = [&](const f32x16& si) __attribute__((always_inline)) {
-        f32x16 sacc = si, pacc = dinit;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          sacc = mfma32(frag_operand<D>(kf, kb, s, lane), qreg[s], sacc);
-          pacc = mfma32(frag_operand<D>(vf, kb, s, lane), doreg[s], pacc);
-        }
-        bf16x8 dsb[2];
-#pragma unroll
-        for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            dqacc[db] = mfma32(lds_operand_tr(kr + (32 * kb + 16 * kk) * D + 32 * db, D, lane), dsb[kk], dqacc[db]);
-      };
-      if ((k0 + 31 <= qw0) && (k0 >= qw0 + 32 - W)) {
-        body(sinit);
-      } else {
-        // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
-        f32x16 si = sinit;
-        const int d0 = myq - k0 - 4 * h32;
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          const int cst = 8 * (x >> 2) + (x & 3);
-          si[x] = (unsigned)(d0 - cst) < (unsigned)W ? si[x] : -INFINITY;
-        }
-        body(si);
+      for (int x = 0; x < 16; ++x) {
+        const int cst = 8 * (x >> 2) + (x & 3);
+        sacc[x] = (unsigned)(d0 - cst) < (unsigned)W ? sacc[x] : -INFINITY;
       }
     }
-  };
-
-  // Triple-buffered: before tile t is read each wave waits for its own copy of
-  // tile t (tile t + 1 may still be in flight); the barrier then makes every
-  // copy visible and frees the buffer of tile t - 1, into which tile t + 2 is
-  // issued at once.
-  auto stage = [&](int t, const bf16* kf, const bf16* kr, const bf16* vf, bf16* kfn, bf16* krn, bf16* vfn)
-                   __attribute__((always_inline)) {
-    if (t + 1 <= t_hi)
-      dma_barrier<PER>();
-    else
-      dma_barrier<0>();
-    if (t + 2 <= t_hi) load_tile(t + 2, kfn, krn, vfn);
-    tile_step(t, kf, kr, vf);
-  };
-  for (int t = t_lo; t <= t_hi; t += 3) {
-    stage(t, kf0, kr0, vf0, kf2, kr2, vf2);
-    if (t + 1 > t_hi) break;
-    stage(t + 1, kf1, kr1, vf1, kf0, kr0, vf0);
-    if (t + 2 > t_hi) break;
-    stage(t + 2, kf2, kr2, vf2, kf1, kr1, vf1);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      sacc = mfma32(cs_operand<D>(kt, off_s[s], 0), qreg[s], sacc);
+      pacc = mfma32(cs_operand<D>(vt, off_s[s], 0), doreg[s], pacc);
+    }
+    bf16x8 dsb[2];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
   }
 
-  if (myq < T) {
-    bf16* dqrow = a.dq + b * a.sdq[0] + h * a.sdq[2] + (int64_t)myq * a.sdq[1];
+  // dQ through LDS: every wave is past its last tile, so wave w may use the
+  // bytes [32 rows * w, 32 rows * (w + 1)) of the ring for its block.
+  dma_barrier<0>();
+  const unsigned reg = lring + wave * (32 * D * 2);
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bf16x4 v4;
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 v4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v4[j] = (bf16)(dqacc[db][4 * i + j] * a.scale);
-        *reinterpret_cast<bf16x4*>(dqrow + 32 * db + 8 * i + 4 * h32) = v4;
-      }
+      for (int j = 0; j < 4; ++j) v4[j] = (bf16)(dqacc[db][4 * i + j] * a.scale);
+      lds_write_b64(reg + L::byte(l32, 4 * db + i) + 8 * h32, v4);
+    }
+  bf16* dqbase = a.dq + b * a.sdq[0] + h * a.sdq[2];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int row = L::dma_row(k, lane);
+    const bf16x8 v = lds_read_b128(reg + L::byte(row, lane % L::U));
+    if (qw0 + row < T) *reinterpret_cast<bf16x8*>(dqbase + (int64_t)(qw0 + row) * a.sdq[1] + 8 * (lane % L::U)) = v;
+  }
+  if (myq < T && h32 == 0) {
+    a.delta[(int64_t)bh * T + myq] = nlse2;
+    a.delta[(int64_t)(a.B * H + bh) * T + myq] = ndelta;
   }
 }
 
@@ -225,18 +275,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 // their use, so that the copies of several tiles are in flight while one is
 // computed; the ring slot advances by counting.
 // ---------------------------------------------------------------------------
-template <int PERW, int K>
-__device__ __forceinline__ void dma_barrier_upto(int newer) {
-  if constexpr (K == 0) {
-    dma_barrier<0>();
-  } else {
-    if (newer >= K)
-      dma_barrier<K * PERW>();
-    else
-      dma_barrier_upto<PERW, K - 1>(newer);
-  }
-}
-
 template <int D, int NBUF>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   constexpr int NW = 4, BNK = NW * 32, BMQ = 32;
@@ -419,11 +457,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
   if (phases & kBwdDq) {
-    constexpr int BM = 4 * 32;
-    constexpr int BN = 32;  // three stages of 32-key K, K^T and V tiles: 36 KB (D = 64) or 72 KB of LDS
+    constexpr int BM = 128;
     const int nqt = (a.T + BM - 1) / BM;
     const int64_t blocks = (int64_t)nqt * a.H * a.B;
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, BN>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    // D = 64: 6 slots of 8 KB, two tiles in flight while the staging (4 slots) is used;
+    // D = 128: 5 slots of 16 KB, one tile in flight.
+    if constexpr (D == 64)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, 6, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, 5, 1>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

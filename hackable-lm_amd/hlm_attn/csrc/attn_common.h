@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace hlm {
 
 typedef __bf16 bf16;
@@ -374,6 +376,157 @@ __device__ __forceinline__ void dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// dma_barrier<K * PERW> for the largest K <= min(newer, KMAX): the barrier of
+// a ring that has `newer` tiles of PERW copies each in flight behind the one
+// being waited for.
+template <int PERW, int KMAX>
+__device__ __forceinline__ void dma_barrier_upto(int newer) {
+  if constexpr (KMAX == 0) {
+    dma_barrier<0>();
+  } else {
+    if (newer >= KMAX)
+      dma_barrier<KMAX * PERW>();
+    else
+      dma_barrier_upto<PERW, KMAX - 1>(newer);
+  }
+}
+
+// Waits (no barrier) until at most K * PERW vector-memory ops of this wave
+// are outstanding, K = min(newer, KMAX).
+template <int PERW, int KMAX>
+__device__ __forceinline__ void vm_wait_upto(int newer) {
+  if constexpr (KMAX == 0) {
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+  } else {
+    if (newer >= KMAX) {
+      constexpr int p = KMAX * PERW;
+      static_assert(p < 64, "vmcnt range");
+      __builtin_amdgcn_s_waitcnt((p & 15) | (7 << 4) | (15 << 8) | ((p >> 4) << 14));
+      asm volatile("" ::: "memory");
+    } else {
+      vm_wait_upto<PERW, KMAX - 1>(newer);
+    }
+  }
+}
+
+// Vector-memory loads issued as inline asm, so that the compiler neither
+// tracks them nor inserts waits for them: the caller waits explicitly
+// (vm_wait_upto) and then calls touch() on each result, which keeps every use
+// of the value behind that wait.
+__device__ __forceinline__ bf16x8 asm_load_b128(__amdgpu_buffer_rsrc_t rs, int voff) {
+  typedef __attribute__((ext_vector_type(4))) int i32x4;
+  i32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ float asm_load_b32(__amdgpu_buffer_rsrc_t rs, int voff) {
+  float v;
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
+  return v;
+}
+template <typename X>
+__device__ __forceinline__ void touch(X& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// Buffer resource over n contiguous fp32 values (reads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* base, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n * 4, 0x00020000);
+}
+
+// ---------------------------------------------------------------------------
+// "cs" tile layout: R rows x D bf16 in LDS, built for coalesced copies.
+//
+// A tile is a sequence of 1 KB chunks of RPC = 512 / D whole rows (8 rows of
+// 128 B for D = 64, 4 rows of 256 B for D = 128).  Within a chunk, 16-byte unit
+// u of row r sits in slot (r % RPC) * U + (u ^ f(r)), U = D / 8 units per row,
+// with an XOR pattern f that depends on r % 16.  Hence:
+//  * one 1 KB DMA instruction copies RPC whole rows (every lane reads 16 bytes
+//    of a row, 8 or 16 lanes cover it contiguously): fully coalesced;
+//  * an MFMA operand along the rows (lane l: row 32 rb + l % 32, unit
+//    2 s + l / 32; one ds_read_b128) and a transposed operand
+//    (ds_read_b64_tr_b16 over 4 rows x 4 units per 32 lanes) are both free of
+//    LDS bank conflicts (64 banks of 4 bytes; 16 lanes per b128 pass,
+//    32 lanes per b64 pass).
+// f: D = 64: bit 2 = bit 1 of r, bits 0-1 = bits 2-3 of r;
+//    D = 128: bits 2-3 = bits 0-1 of r, bits 0-1 = bits 2-3 of r.
+// ---------------------------------------------------------------------------
+template <int D>
+struct CS {
+  static constexpr int U = D / 8;      // 16-byte units per row
+  static constexpr int RPC = 512 / D;  // rows per 1 KB chunk
+  static constexpr int ROW32 = 32 * 2 * D;  // bytes of 32 rows
+  __device__ __forceinline__ static int f(int r) {
+    if constexpr (D == 64)
+      return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else
+      return ((r & 3) << 2) | ((r >> 2) & 3);
+  }
+  // Byte offset of unit u of row r.
+  __device__ __forceinline__ static int byte(int r, int u) {
+    return (r / RPC) * 1024 + ((r % RPC) * U + (u ^ f(r))) * 16;
+  }
+  // Copy of chunk j: lane l reads 16 bytes of row RPC j + l / U at this byte
+  // offset within the row (add (row0 + RPC j + l / U) * row stride).
+  __device__ __forceinline__ static int dma_row(int j, int lane) { return RPC * j + lane / U; }
+  __device__ __forceinline__ static int dma_col_bytes(int j, int lane) {
+    return ((lane % U) ^ f(RPC * j + lane / U)) * 16;
+  }
+};
+
+// Operand along the rows of a cs tile at LDS byte address `base`: lane l gets
+// row 32 rb + l % 32, columns 16 s + 8 (l / 32) .. + 7 (the A/B layout of a
+// 32x32x16 MFMA).  `off_s` = CS<D>::byte(l % 32, 2 s + l / 32), precomputed.
+template <int D>
+__device__ __forceinline__ bf16x8 cs_operand(unsigned base, int off_s, int rb) {
+  typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+  return *(const lds_bf16x8*)(uintptr_t)(base + off_s + rb * CS<D>::ROW32);
+}
+
+// Per-lane byte offsets of the transposed operand of a cs tile for the 32
+// columns c0 = 32 db: the two ds_read_b64_tr_b16 of rows 4 (g / 2) + rr and
+// +8 (g = l / 16, rr = (l / 4) % 4), 8-byte piece 16 (g % 2) + 4 (l % 4) of
+// the column block.
+template <int D>
+__device__ __forceinline__ int cs_tr_off(int db, int second, int lane) {
+  const int g = lane >> 4, rr = (lane >> 2) & 3, c = lane & 3;
+  const int row = 4 * (g >> 1) + rr + 8 * second;
+  const int col = 32 * db + 16 * (g & 1) + 4 * c;
+  return CS<D>::byte(row, col >> 3) + 8 * ((col >> 2) & 1);
+}
+
+// Transposed operand of a cs tile, contracting over the 16 rows r0 .. r0 + 15
+// (r0 a multiple of 16) for 32 columns: lane l receives the values of column
+// l % 32 at rows sigma(8 (l / 32) + e) (the order of lds_operand_tr).  o0, o1 =
+// cs_tr_off(db, 0 / 1, lane).
+template <int D>
+__device__ __forceinline__ bf16x8 cs_operand_tr(unsigned base, int o0, int o1, int r0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const unsigned rb = base + r0 * 2 * D;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(rb + o0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(rb + o1));
+  const bf16x4 lo_b = __builtin_bit_cast(bf16x4, lo);
+  const bf16x4 hi_b = __builtin_bit_cast(bf16x4, hi);
+  bf16x8 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    out[e] = lo_b[e];
+    out[4 + e] = hi_b[e];
+  }
+  return out;
+}
+
+// Plain LDS access at a byte address.
+__device__ __forceinline__ bf16x8 lds_read_b128(unsigned addr) {
+  typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+  return *(const lds_bf16x8*)(uintptr_t)addr;
+}
+__device__ __forceinline__ void lds_write_b64(unsigned addr, bf16x4 v) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  *(lds_bf16x4*)(uintptr_t)addr = v;
+}
+
 // Waits for every outstanding vector-memory op of this wave.  Used once after
 // a kernel's prologue loads (and stores), so that inside the DMA-pipelined
 // loop the compiler has nothing of its own left to wait for and dma_barrier's
@@ -384,6 +537,38 @@ __device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70
 template <int D>
 __device__ __forceinline__ bf16x8 frag_operand(const bf16* lds, int rb, int s, int lane) {
   return *reinterpret_cast<const bf16x8*>(lds + (rb * (D / 16) + s) * 512 + lane * 8);
+}
+
+// Workgroups of a persistent launch: as many as the device holds at once
+// (occupancy x compute units), at most n_items, rounded down to a multiple of 8
+// (the XCD count) when that is at least 8.  Cached per kernel and device.
+inline int persistent_grid(const void* kernel, int block, int64_t n_items) {
+  struct Entry {
+    const void* kernel;
+    int device, grid;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int n_cache = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  int full = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cache; ++i)
+      if (cache[i].kernel == kernel && cache[i].device == dev) full = cache[i].grid;
+  }
+  if (full == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    full = per_cu * cus;
+    std::lock_guard<std::mutex> lock(mu);
+    if (n_cache < 64) cache[n_cache++] = {kernel, dev, full};
+  }
+  int64_t g = n_items < full ? n_items : full;
+  if (g >= 8) g &= ~(int64_t)7;
+  return (int)(g > 0 ? g : 1);
 }
 
 }  // namespace hlm
