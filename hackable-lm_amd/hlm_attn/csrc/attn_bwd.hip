@@ -65,12 +65,22 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 //    delta = rowsum(dO * O) together with the staged dO.
 //  * dQ leaves through LDS: each wave writes its 32 x D block into a cs tile
 //    and stores whole rows.
-// Every vector-memory load is inline asm with explicit waits (the compiler
-// tracks none of them) and no store is issued before the loop ends, so inside
-// the loop the vector-memory counter counts tile copies only.
+// Tile and staging copies are inline asm with explicit waits; the few loads
+// into registers are ordinary (compiler-tracked) buffer loads issued before
+// them, and no store is issued before the loop ends, so inside the loop the
+// vector-memory counter counts tile copies only.
 // ---------------------------------------------------------------------------
+#ifndef HLM_DQZ
+#define HLM_DQZ 0
+#endif
+#ifndef HLM_DQ_MINB
+#define HLM_DQ_MINB 2
+#endif
+#ifndef HLM_DQ_PRIO
+#define HLM_DQ_PRIO 0
+#endif
 template <int D, int NBUF, int PRE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256, HLM_DQ_MINB) void attn_bwd_dq_kernel(BwdArgs a) {
   using L = CS<D>;
   constexpr int NW = 4, BM = NW * 32, BN = 32;
   constexpr int NDB = D / 32, NS = D / 16;
@@ -81,6 +91,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   constexpr int NCH = 32 / L::RPC;        // chunks of a wave's 32 rows
   constexpr int WSTG = 2 * NCH * 1024;    // staging bytes per wave (Q and dO)
   static_assert(CPT % NW == 0, "tile chunks split evenly over the waves");
+  static_assert(PRE >= 1, "the loop waits for tile 0 at its first barrier");
   static_assert(PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
   static_assert(NBUF * PER < 64 && 2 * NCH + PRE * PER < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
@@ -114,8 +125,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   bf16x8 oc[NCH];
 #pragma unroll
   for (int k = 0; k < NCH; ++k)
-    oc[k] = asm_load_b128(ro, (qw0 + L::dma_row(k, lane)) * so2 + (lane % L::U) * 16);
-  float lraw = asm_load_b32(rl, myq * 4);  // 0 for rows >= T
+    oc[k] = buf_load_b128(ro, (qw0 + L::dma_row(k, lane)) * so2 + (lane % L::U) * 16);
+  float lraw = buf_load_b32(rl, myq * 4);  // 0 for rows >= T
   // 2. Its Q and dO rows into the staging area (cs layout).
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
@@ -149,9 +160,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 
   // 4. Wait for this wave's rows (the first tiles may still be in flight).
   vm_wait_upto<PER, PRE>(n_pre);
-#pragma unroll
-  for (int k = 0; k < NCH; ++k) touch(oc[k]);
-  touch(lraw);
 
   int off_s[NS];
 #pragma unroll
@@ -213,6 +221,52 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
     const int k0 = (t_lo + it) * BN;
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
+#if HLM_DQZ
+    // All K and V operands of the tile first, then the S and dP chains from
+    // zero; -lse * log2(e) and -delta are added by the VALU.
+    bf16x8 kop[NS], vop[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      kop[s] = cs_operand<D>(kt, off_s[s], 0);
+      vop[s] = cs_operand<D>(vt, off_s[s], 0);
+    }
+    f32x16 sacc = zero16(), pacc = zero16();
+    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      sacc = mfma32(kop[s], qreg[s], sacc);
+      pacc = mfma32(vop[s], doreg[s], pacc);
+    }
+    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(0);
+    bf16x8 ktr[2][NDB];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) ktr[kk][db] = cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk);
+    float sv[16];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) sv[x] = sacc[x] + nlse2;
+    if (!full) {
+      // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
+      const int d0 = myq - k0 - 4 * h32;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int cst = 8 * (x >> 2) + (x & 3);
+        sv[x] = (unsigned)(d0 - cst) < (unsigned)W ? sv[x] : -INFINITY;
+      }
+    }
+    bf16x8 dsb[2];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sv[x]) * (pacc[x] + ndelta));
+    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) dqacc[db] = mfma32(ktr[kk][db], dsb[kk], dqacc[db]);
+    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(0);
+  }
+
+#else
     f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
     if (!full) {
       // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
@@ -238,9 +292,16 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
         dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
   }
 
+#endif
   // dQ through LDS: every wave is past its last tile, so wave w may use the
   // bytes [32 rows * w, 32 rows * (w + 1)) of the ring for its block.
   dma_barrier<0>();
+  // The epilogue's addresses derive from a lane index that the compiler cannot
+  // see through, so they are computed here rather than hoisted (and kept live)
+  // above the loop.
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int e32 = ln & 31, eh = ln >> 5;
   const unsigned reg = lring + wave * (32 * D * 2);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -249,14 +310,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
       bf16x4 v4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) v4[j] = (bf16)(dqacc[db][4 * i + j] * a.scale);
-      lds_write_b64(reg + L::byte(l32, 4 * db + i) + 8 * h32, v4);
+      lds_write_b64(reg + L::byte(e32, 4 * db + i) + 8 * eh, v4);
     }
   bf16* dqbase = a.dq + b * a.sdq[0] + h * a.sdq[2];
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
-    const int row = L::dma_row(k, lane);
-    const bf16x8 v = lds_read_b128(reg + L::byte(row, lane % L::U));
-    if (qw0 + row < T) *reinterpret_cast<bf16x8*>(dqbase + (int64_t)(qw0 + row) * a.sdq[1] + 8 * (lane % L::U)) = v;
+    const int row = L::dma_row(k, ln);
+    const bf16x8 v = lds_read_b128(reg + L::byte(row, ln % L::U));
+    if (qw0 + row < T) *reinterpret_cast<bf16x8*>(dqbase + (int64_t)(qw0 + row) * a.sdq[1] + 8 * (ln % L::U)) = v;
   }
   if (myq < T && h32 == 0) {
     a.delta[(int64_t)bh * T + myq] = nlse2;
@@ -269,30 +330,48 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 // multiplied by scale * log2(e), and V stay in VGPRs as B operands); the start
 // values of the S and dP accumulators, -lse * log2(e) and -delta of the query
 // rows, come from LDS.  dV^T += dO^T P and dK^T += Q^T dS read dO^T / Q^T
-// transposed from the same swizzled copies that feed S and dP.
+// transposed from the same cs-layout copies that feed S and dP.
 //
-// Query tiles stream through an NBUF-stage LDS ring, NBUF - 1 tiles ahead of
-// their use, so that the copies of several tiles are in flight while one is
-// computed; the ring slot advances by counting.
+// Every global access is coalesced: query tiles (Q, dO: 32 rows) stream
+// through an NBUF-slot LDS ring as whole-row DMA in the cs layout; each wave's
+// own K and V rows arrive the same way in ring slots the ring does not use yet
+// (PRE tiles are in flight in the first slots), and dK, dV leave through LDS
+// as whole rows.  The ring is topped up to NBUF - 1 tiles ahead after each
+// barrier.
 // ---------------------------------------------------------------------------
-template <int D, int NBUF>
+#ifndef HLM_DKDV_KEEP
+#define HLM_DKDV_KEEP 0
+#endif
+#ifndef HLM_DKDV_INTERLEAVE
+#define HLM_DKDV_INTERLEAVE 0
+#endif
+template <int D, int NBUF, int PRE>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
+  using L = CS<D>;
   constexpr int NW = 4, BNK = NW * 32, BMQ = 32;
   constexpr int NDB = D / 32, NS = D / 16;
-  constexpr int TILE = BMQ * D;
-  constexpr int PER = 2 * TILE / 512 / NW;  // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
-  static_assert(NBUF >= 3, "at least one tile in flight while one is computed");
-  __shared__ __attribute__((aligned(1024))) bf16 qbuf[NBUF][TILE];
-  __shared__ __attribute__((aligned(1024))) bf16 dbuf[NBUF][TILE];
+  constexpr int TILEB = BMQ * D * 2;     // bytes of one Q or dO tile
+  constexpr int SLOTB = 2 * TILEB;       // one ring slot: Q and dO
+  constexpr int CPT = TILEB / 1024;      // 1 KB chunks per tile
+  constexpr int PER = 2 * CPT / NW;      // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
+  constexpr int NCH = 32 / L::RPC;       // chunks of a wave's 32 rows
+  constexpr int WSTG = 2 * NCH * 1024;   // staging bytes per wave (K and V)
+  // D = 64: K and V rows arrive by whole-row DMA into ring slots and are read
+  // from there; D = 128: each lane loads its own row pieces (the ring then
+  // keeps its slots for query tiles from the start).
+  constexpr bool STAGE_KV = D == 64;
+  static_assert(CPT % NW == 0, "tile chunks split evenly over the waves");
+  static_assert(!STAGE_KV || PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
+  static_assert(PRE >= 1 && PRE < NBUF, "tile 0 is in flight before the loop");
+  static_assert(NBUF * (PER + 1) < 64 && 2 * NS + 2 * NCH + PRE * (PER + 1) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
   __shared__ __attribute__((aligned(256))) float stbuf[NBUF][128];  // [0, 64): -lse * log2(e), [64, 128): -delta
 
   const int T = a.T, W = a.W, H = a.H, Hkv = a.Hkv;
   const int G = H / Hkv;
-  const int nkt = (T + BNK - 1) / BNK;
-  // Rank-major (measured faster here than the two-phase order): every kv
-  // head's longest key tiles first.
+  // Rank-major: every kv head's longest key tiles (the low ones) first.
   const TileId tid_ = rank_major(blockIdx.x, a.B * Hkv);
-  const int kt = tid_.rank;  // low key tiles see the most queries: they go first
+  const int kt = tid_.rank;
   const int bhk = tid_.unit;
   const int hk = bhk % Hkv, b = bhk / Hkv;
 
@@ -308,11 +387,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   const int n_iter = nq * G;
   const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2);
 
-  // Tiles are visited head by head (the G query heads of this kv head), query
-  // tile by query tile; the copy pointer (ld_*) runs NBUF - 1 tiles ahead of
-  // the compute pointer.  Its buffer resources walk down the slabs by one
-  // tile per copy.
-  int ld_g = 0, ld_t = 0, ld_slot = 0;
+  const unsigned lring = lds_addr(ring), lst = lds_addr(stbuf) + 256 * wave;
+  const unsigned stg_k = lring + PRE * SLOTB + wave * WSTG, stg_v = stg_k + NCH * 1024;
+
+  // 1. This wave's K and V rows: into the staging area (cs layout), or
+  // straight into registers as B operands (lane l: row kw0 + l % 32, columns
+  // 16 s + 8 (l / 32) + e).
+  bf16x8 kraw[NS], vraw[NS];
+  {
+    const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
+    const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
+    const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
+    if constexpr (STAGE_KV) {
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int row = kw0 + L::dma_row(k, lane), cb = L::dma_col_bytes(k, lane);
+        lds_dma_at<16>(rk, stg_k + k * 1024, row * sk2 + cb);
+        lds_dma_at<16>(rv, stg_v + k * 1024, row * sv2 + cb);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kraw[s] = buf_load_b128(rk, mykey * sk2 + (16 * s + 8 * h32) * 2);
+        vraw[s] = buf_load_b128(rv, mykey * sv2 + (16 * s + 8 * h32) * 2);
+      }
+    }
+  }
+
+  // 2. Query tiles, visited head by head (the G query heads of this kv head),
+  // tile by tile; each copy goes to ring slot (issue index) % NBUF.  The
+  // buffer resources walk down the slabs by one tile per copy.
+  int ld_g = 0, ld_t = 0, issued = 0;
   const int64_t qstep = (int64_t)BMQ * a.sq[1] * 2, dostep = (int64_t)BMQ * a.sdo[1] * 2;
   const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;  // waves 0 / 1 copy -lse*log2(e) / -delta
   SlabCursor cq, cdo, cst;
@@ -323,14 +428,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     cst = {(uint64_t)(uintptr_t)(a.delta + plane + ((int64_t)b * H + hq) * T + qs), (int64_t)(T - qs) * 4};
   };
   start_head();
-  const SwzOffsets<BMQ, D, NW> oq = swz_offsets<BMQ, D, NW>(sq2, wave, lane);
-  const SwzOffsets<BMQ, D, NW> odo = swz_offsets<BMQ, D, NW>(sdo2, wave, lane);
-  const unsigned lq = lds_addr(qbuf), ldo = lds_addr(dbuf), lst = lds_addr(stbuf) + 256 * wave;
+  int qof[CPT / NW], dof[CPT / NW];
+#pragma unroll
+  for (int i = 0; i < CPT / NW; ++i) {
+    const int j = wave + NW * i;
+    qof[i] = L::dma_row(j, lane) * sq2 + L::dma_col_bytes(j, lane);
+    dof[i] = L::dma_row(j, lane) * sdo2 + L::dma_col_bytes(j, lane);
+  }
   auto load_tile = [&]() __attribute__((always_inline)) {
-    dma_swz_at<BMQ, D, NW>(cq.rsrc(), oq, lq + ld_slot * (TILE * 2), wave);
-    dma_swz_at<BMQ, D, NW>(cdo.rsrc(), odo, ldo + ld_slot * (TILE * 2), wave);
-    if (wave < 2) lds_dma_at<4>(cst.rsrc(), lst + ld_slot * 512, lane * 4);  // fp32 rows, 64 lanes x 4 bytes
-    if (++ld_slot == NBUF) ld_slot = 0;
+    const int slot = issued % NBUF;
+    const unsigned sb = lring + (unsigned)slot * SLOTB;
+    const __amdgpu_buffer_rsrc_t rq = cq.rsrc(), rdo = cdo.rsrc();
+#pragma unroll
+    for (int i = 0; i < CPT / NW; ++i) {
+      const unsigned piece = (unsigned)(wave + NW * i) * 1024;
+      lds_dma_at<16>(rq, sb + piece, qof[i]);
+      lds_dma_at<16>(rdo, sb + TILEB + piece, dof[i]);
+    }
+    if (wave < 2) lds_dma_at<4>(cst.rsrc(), lst + slot * 512, lane * 4);  // fp32 rows, 64 lanes x 4 bytes
+    ++issued;
     if (++ld_t == nq) {
       ld_t = 0;
       ++ld_g;
@@ -341,22 +457,43 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
       cst.advance(BMQ * 4);
     }
   };
+  const int n_pre = min(PRE, n_iter);
+  for (int i = 0; i < n_pre; ++i) load_tile();
 
+  // 3. Wait for this wave's K and V rows (the first tiles may be in flight).
+  if (wave < 2)
+    vm_wait_upto<PER + 1, PRE>(n_pre);
+  else
+    vm_wait_upto<PER, PRE>(n_pre);
+
+  // Operand offsets: kept in registers for D = 64, recomputed per use for
+  // D = 128 (whose accumulators leave no room for them).
+  constexpr bool KEEP_TRO = D == 64 || HLM_DKDV_KEEP;
+  const int rbase = (l32 / L::RPC) * 1024 + (l32 % L::RPC) * L::U * 16, fr = L::f(l32);
+  int off_s[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) off_s[s] = KEEP_TRO ? L::byte(l32, 2 * s + h32) : 0;
+  auto offs = [&](int s) __attribute__((always_inline)) {
+    return KEEP_TRO ? off_s[s] : rbase + (((2 * s + h32) ^ fr) << 4);
+  };
+  int tro[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tro[db][0] = KEEP_TRO ? cs_tr_off<D>(db, 0, lane) : 0;
+    tro[db][1] = KEEP_TRO ? cs_tr_off<D>(db, 1, lane) : 0;
+  }
   // K^T (times scale * log2(e)) and V^T as B operands: lane l holds row
   // kw0 + l % 32, columns 16 s + 8 (l / 32) + e.
   bf16x8 kreg[NS], vreg[NS];
-  {
-    const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
-    const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
-    const int sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      kreg[s] = scale_bf16x8(slab_load(rk, mykey, sk2, 16 * s + 8 * h32), c);
-      vreg[s] = slab_load(rv, mykey, sv2, 16 * s + 8 * h32);
+  for (int s = 0; s < NS; ++s) {
+    if constexpr (STAGE_KV) {
+      kraw[s] = cs_operand<D>(stg_k, offs(s), 0);
+      vraw[s] = cs_operand<D>(stg_v, offs(s), 0);
     }
+    kreg[s] = scale_bf16x8(kraw[s], c);
+    vreg[s] = vraw[s];
   }
-  drain_vmem();
-  for (int i = 0; i < NBUF - 1 && i < n_iter; ++i) load_tile();
 
   f32x16 dkacc[NDB], dvacc[NDB];
 #pragma unroll
@@ -367,25 +504,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
   const bool wave_live = kw0 < T;
   const int wk_hi = min(kw0 + 31, T - 1);
-  int cp_t = 0, cp_slot = 0;  // query tile (within the current head) and ring slot of the compute pointer
+  int cp_t = 0;  // query tile (within the current head) of the compute pointer
 
   for (int it = 0; it < n_iter; ++it) {
-    // Wait for this wave's copies of tile it (the newer tiles may stay in
-    // flight); the barrier makes every wave's copies visible and frees the
-    // slot of tile it - 1, which takes tile it + NBUF - 1.
-    const int newer = min(NBUF - 2, n_iter - 1 - it);
+    // Wait for this wave's copies of tile it (newer tiles may stay in flight);
+    // the barrier makes every wave's copies visible and frees the slot of tile
+    // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
+    // NBUF - 1 tiles ahead.
     if (wave < 2)
-      dma_barrier_upto<PER + 1, NBUF - 2>(newer);
+      dma_barrier_upto<PER + 1, NBUF - 1>(issued - 1 - it);
     else
-      dma_barrier_upto<PER, NBUF - 2>(newer);
-    if (it + NBUF - 1 < n_iter) load_tile();
+      dma_barrier_upto<PER, NBUF - 1>(issued - 1 - it);
+    const int want = min(it + NBUF, n_iter);
+    while (issued < want) load_tile();
 
-    const bf16* qs_t = qbuf[cp_slot];
-    const bf16* ds_t = dbuf[cp_slot];
-    const float* st = stbuf[cp_slot];
+    const int slot = it % NBUF;
+    const unsigned qs_t = lring + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
+    const float* st = stbuf[slot];
     const int qs = (tq_lo + cp_t) * BMQ;
     if (++cp_t == nq) cp_t = 0;
-    if (++cp_slot == NBUF) cp_slot = 0;
     if (!(wave_live && qs <= wk_hi + W - 1 && qs + BMQ - 1 >= kw0)) continue;
     // Query rows >= T need no mask: their Q, dO and start values arrive as
     // zeros, so they add exactly zero to dK and dV.
@@ -416,9 +553,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     f32x16 sacc = si, pacc = di;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      sacc = mfma32(swz_operand<D>(qs_t, 0, s, lane), kreg[s], sacc);
-      pacc = mfma32(swz_operand<D>(ds_t, 0, s, lane), vreg[s], pacc);
+      const int o = offs(s);
+      sacc = mfma32(cs_operand<D>(qs_t, o, 0), kreg[s], sacc);
+      pacc = mfma32(cs_operand<D>(ds_t, o, 0), vreg[s], pacc);
     }
+#if HLM_DKDV_INTERLEAVE
+    if constexpr (D == 128) {
+      // Keep the operand reads next to their MFMAs (two reads ahead), so that
+      // the 16 operands of a tile are not all live at once.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int s = 0; s < NS - 2; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+#endif
     bf16x8 pb[2], dsb[2];
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
@@ -430,27 +581,45 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        dvacc[db] = mfma32(swz_operand_tr<D>(ds_t, 16 * kk, 32 * db, lane), pb[kk], dvacc[db]);
-        dkacc[db] = mfma32(swz_operand_tr<D>(qs_t, 16 * kk, 32 * db, lane), dsb[kk], dkacc[db]);
+        const int o0 = KEEP_TRO ? tro[db][0] : cs_tr_off<D>(db, 0, lane);
+        const int o1 = KEEP_TRO ? tro[db][1] : cs_tr_off<D>(db, 1, lane);
+        dvacc[db] = mfma32(cs_operand_tr<D>(ds_t, o0, o1, 16 * kk), pb[kk], dvacc[db]);
+        dkacc[db] = mfma32(cs_operand_tr<D>(qs_t, o0, o1, 16 * kk), dsb[kk], dkacc[db]);
       }
   }
 
-  if (mykey < T) {
-    bf16* dkrow = a.dk + b * a.sdk[0] + hk * a.sdk[2] + (int64_t)mykey * a.sdk[1];
-    bf16* dvrow = a.dv + b * a.sdv[0] + hk * a.sdv[2] + (int64_t)mykey * a.sdv[1];
+  // dK and dV through LDS: every wave is past its last tile, so wave w may use
+  // the bytes [64 rows * w, 64 rows * (w + 1)) of the ring for its two blocks.
+  dma_barrier<0>();
+  // Epilogue addresses from an opaque lane index (computed here, not hoisted).
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int e32 = ln & 31, eh = ln >> 5;
+  const unsigned rk_ = lring + wave * (2 * 32 * D * 2), rv_ = rk_ + 32 * D * 2;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bf16x4 k4, v4;
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 k4, v4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          k4[j] = (bf16)(dkacc[db][4 * i + j] * a.scale);
-          v4[j] = (bf16)dvacc[db][4 * i + j];
-        }
-        *reinterpret_cast<bf16x4*>(dkrow + 32 * db + 8 * i + 4 * h32) = k4;
-        *reinterpret_cast<bf16x4*>(dvrow + 32 * db + 8 * i + 4 * h32) = v4;
+      for (int j = 0; j < 4; ++j) {
+        k4[j] = (bf16)(dkacc[db][4 * i + j] * a.scale);
+        v4[j] = (bf16)dvacc[db][4 * i + j];
       }
+      const int ub = L::byte(e32, 4 * db + i) + 8 * eh;
+      lds_write_b64(rk_ + ub, k4);
+      lds_write_b64(rv_ + ub, v4);
+    }
+  bf16* dkbase = a.dk + b * a.sdk[0] + hk * a.sdk[2];
+  bf16* dvbase = a.dv + b * a.sdv[0] + hk * a.sdv[2];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int row = L::dma_row(k, ln), ub = L::byte(row, ln % L::U);
+    const bf16x8 kv = lds_read_b128(rk_ + ub), vv = lds_read_b128(rv_ + ub);
+    if (kw0 + row < T) {
+      *reinterpret_cast<bf16x8*>(dkbase + (int64_t)(kw0 + row) * a.sdk[1] + 8 * (ln % L::U)) = kv;
+      *reinterpret_cast<bf16x8*>(dvbase + (int64_t)(kw0 + row) * a.sdv[1] + 8 * (ln % L::U)) = vv;
+    }
   }
 }
 
@@ -473,10 +642,13 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases) {
     constexpr int BNK = 4 * 32;
     const int nkt = (a.T + BNK - 1) / BNK;
     const int64_t blocks = (int64_t)nkt * a.Hkv * a.B;
-    // Six stages (51 KB) for D = 64, four (66 KB) for D = 128: two or three
-    // workgroups per CU either way.
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, D == 64 ? 6 : 4>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                       stream, a);
+    // D = 64: six slots of 8 KB (three workgroups per CU), the K/V staging in
+    // four of them behind two tiles in flight; D = 128: four slots of 16 KB
+    // (two per CU), three tiles in flight from the start.
+    if constexpr (D == 64)
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, 6, 2>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, 4, 3>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
   }
   return hipSuccess;

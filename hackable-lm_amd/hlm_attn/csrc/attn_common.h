@@ -410,24 +410,14 @@ __device__ __forceinline__ void vm_wait_upto(int newer) {
   }
 }
 
-// Vector-memory loads issued as inline asm, so that the compiler neither
-// tracks them nor inserts waits for them: the caller waits explicitly
-// (vm_wait_upto) and then calls touch() on each result, which keeps every use
-// of the value behind that wait.
-__device__ __forceinline__ bf16x8 asm_load_b128(__amdgpu_buffer_rsrc_t rs, int voff) {
+// Ordinary (compiler-tracked) buffer loads at a byte offset; reads past the
+// resource's extent return zeros.
+__device__ __forceinline__ bf16x8 buf_load_b128(__amdgpu_buffer_rsrc_t rs, int voff) {
   typedef __attribute__((ext_vector_type(4))) int i32x4;
-  i32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
-  return __builtin_bit_cast(bf16x8, v);
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0));
 }
-__device__ __forceinline__ float asm_load_b32(__amdgpu_buffer_rsrc_t rs, int voff) {
-  float v;
-  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
-  return v;
-}
-template <typename X>
-__device__ __forceinline__ void touch(X& x) {
-  asm volatile("" : "+v"(x));
+__device__ __forceinline__ float buf_load_b32(__amdgpu_buffer_rsrc_t rs, int voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 0, 0));
 }
 
 // Buffer resource over n contiguous fp32 values (reads past the end return 0).
