@@ -9,15 +9,14 @@
 //
 // Two kernels, no atomics (fp32 atomics run at ~1.3 TB/s on the MI355X, far
 // too slow to accumulate dQ across key blocks):
-//   attn_bwd_dq_kernel    query-stationary, 32 queries per wave.  Writes the
-//                         workspace the next kernel reads (-lse * log2(e) and
-//                         -delta per query row) and dQ.
+//   attn_bwd_dq_kernel    query-stationary, 32 queries per wave, 128 per
+//                         workgroup.  Writes dQ and the workspace the next
+//                         kernel reads (-lse * log2(e) and -delta per row).
 //   attn_bwd_dkdv_kernel  key-stationary, 32 keys per wave, 128 per
 //                         workgroup, for one kv head; loops over the query
 //                         heads of its group and the 32-row query tiles that
 //                         can see its keys, accumulating dK and dV in VGPRs.
-// Both skip whole tiles outside the causal window, so cost scales with T * W,
-// and both fit two waves per SIMD (at most 256 VGPRs).
+// Both skip whole tiles outside the causal window, so cost scales with T * W.
 //
 // Per score element the VALU does two operations (exp2, multiply) plus two
 // half bf16 conversions:
@@ -30,10 +29,13 @@
 // * on tiles that cross the diagonal or the window edge, masked entries of the
 //   S accumulator's start value are set to -inf (P = 0 there), before the
 //   MFMAs and independent of them.
-// Tiles reach LDS by buffer DMA into named buffers (triple- or double-
-// buffered, loop unrolled accordingly), fragment-major for operands read along
-// their rows and row-major for operands read transposed with
-// ds_read_b64_tr_b16.
+//
+// Memory: every global access is coalesced (whole rows per instruction).
+// Moving tiles stream through an NBUF-slot LDS ring as whole-row DMA in the cs
+// layout (attn_common.h), which serves both the operand read along the rows
+// and the transposed one (ds_read_b64_tr_b16) from one copy; each wave's own
+// rows arrive the same way in ring slots the ring does not use yet; results
+// leave through LDS as whole rows.
 #include "attn_common.h"
 
 namespace hlm {
@@ -70,17 +72,8 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 // them, and no store is issued before the loop ends, so inside the loop the
 // vector-memory counter counts tile copies only.
 // ---------------------------------------------------------------------------
-#ifndef HLM_DQZ
-#define HLM_DQZ 0
-#endif
-#ifndef HLM_DQ_MINB
-#define HLM_DQ_MINB 2
-#endif
-#ifndef HLM_DQ_PRIO
-#define HLM_DQ_PRIO 0
-#endif
 template <int D, int NBUF, int PRE>
-__global__ __launch_bounds__(256, HLM_DQ_MINB) void attn_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
   using L = CS<D>;
   constexpr int NW = 4, BM = NW * 32, BN = 32;
   constexpr int NDB = D / 32, NS = D / 16;
@@ -221,52 +214,6 @@ __global__ __launch_bounds__(256, HLM_DQ_MINB) void attn_bwd_dq_kernel(BwdArgs a
     const int k0 = (t_lo + it) * BN;
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
-#if HLM_DQZ
-    // All K and V operands of the tile first, then the S and dP chains from
-    // zero; -lse * log2(e) and -delta are added by the VALU.
-    bf16x8 kop[NS], vop[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      kop[s] = cs_operand<D>(kt, off_s[s], 0);
-      vop[s] = cs_operand<D>(vt, off_s[s], 0);
-    }
-    f32x16 sacc = zero16(), pacc = zero16();
-    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      sacc = mfma32(kop[s], qreg[s], sacc);
-      pacc = mfma32(vop[s], doreg[s], pacc);
-    }
-    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(0);
-    bf16x8 ktr[2][NDB];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) ktr[kk][db] = cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk);
-    float sv[16];
-#pragma unroll
-    for (int x = 0; x < 16; ++x) sv[x] = sacc[x] + nlse2;
-    if (!full) {
-      // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
-      const int d0 = myq - k0 - 4 * h32;
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const int cst = 8 * (x >> 2) + (x & 3);
-        sv[x] = (unsigned)(d0 - cst) < (unsigned)W ? sv[x] : -INFINITY;
-      }
-    }
-    bf16x8 dsb[2];
-#pragma unroll
-    for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sv[x]) * (pacc[x] + ndelta));
-    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) dqacc[db] = mfma32(ktr[kk][db], dsb[kk], dqacc[db]);
-    if (HLM_DQ_PRIO) __builtin_amdgcn_s_setprio(0);
-  }
-
-#else
     f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
     if (!full) {
       // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
@@ -292,7 +239,6 @@ __global__ __launch_bounds__(256, HLM_DQ_MINB) void attn_bwd_dq_kernel(BwdArgs a
         dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
   }
 
-#endif
   // dQ through LDS: every wave is past its last tile, so wave w may use the
   // bytes [32 rows * w, 32 rows * (w + 1)) of the ring for its block.
   dma_barrier<0>();
@@ -339,12 +285,6 @@ __global__ __launch_bounds__(256, HLM_DQ_MINB) void attn_bwd_dq_kernel(BwdArgs a
 // as whole rows.  The ring is topped up to NBUF - 1 tiles ahead after each
 // barrier.
 // ---------------------------------------------------------------------------
-#ifndef HLM_DKDV_KEEP
-#define HLM_DKDV_KEEP 0
-#endif
-#ifndef HLM_DKDV_INTERLEAVE
-#define HLM_DKDV_INTERLEAVE 0
-#endif
 template <int D, int NBUF, int PRE>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   using L = CS<D>;
@@ -468,7 +408,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
   // Operand offsets: kept in registers for D = 64, recomputed per use for
   // D = 128 (whose accumulators leave no room for them).
-  constexpr bool KEEP_TRO = D == 64 || HLM_DKDV_KEEP;
+  constexpr bool KEEP_TRO = D == 64;
   const int rbase = (l32 / L::RPC) * 1024 + (l32 % L::RPC) * L::U * 16, fr = L::f(l32);
   int off_s[NS];
 #pragma unroll
@@ -557,19 +497,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
       sacc = mfma32(cs_operand<D>(qs_t, o, 0), kreg[s], sacc);
       pacc = mfma32(cs_operand<D>(ds_t, o, 0), vreg[s], pacc);
     }
-#if HLM_DKDV_INTERLEAVE
-    if constexpr (D == 128) {
-      // Keep the operand reads next to their MFMAs (two reads ahead), so that
-      // the 16 operands of a tile are not all live at once.
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int s = 0; s < NS - 2; ++s) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    }
-#endif
     bf16x8 pb[2], dsb[2];
 #pragma unroll
     for (int x = 0; x < 16; ++x) {

@@ -19,14 +19,12 @@
 //   acc[8 t .. 8 t + 7] of a 32-row block, taken as the 8 B-operand values of
 //   contraction step t, cover the rows sigma(8 * (l / 32) + e) of the 16-row
 //   group 16 t .. 16 t + 15 with sigma = [0,1,2,3,8,9,10,11,4,5,6,7,12,13,14,15].
-//   lds_operand_tr() reads the other operand of that contraction in the same
+//   cs_operand_tr() reads the other operand of that contraction in the same
 //   order, so the pair contracts over the right rows without any shuffle.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-
-#include <mutex>
 
 namespace hlm {
 
@@ -41,12 +39,6 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kThreads = 256;  // 4 waves of 64
-
-// 32-query blocks per forward wave (1 or 2); a build-time choice.
-#ifndef HLM_FWD_QB
-#define HLM_FWD_QB 1
-#endif
-constexpr int kFwdQB = HLM_FWD_QB;
 
 // Backward phases (bit mask): dQ + delta first, then dK/dV, which reads delta.
 constexpr int kBwdDq = 1;
@@ -94,13 +86,6 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-__device__ __forceinline__ bf16x8 zero_bf16x8() {
-  bf16x8 z;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
-  return z;
-}
-
 // Workgroup order.  The grid is rank-major: workgroup id = rank * n_units +
 // unit, where a unit is one (batch, head) slab and rank 0 is the unit's
 // longest tile.  The hardware dispatches ids in increasing order, so the
@@ -126,35 +111,6 @@ __device__ __forceinline__ TileId tile_order(int id, int n_units, int n_full) {
   return {n_full + s2 / per, 8 * (s2 % per) + xcd};
 }
 
-// A/B operand whose 8 contraction values sit contiguously in one LDS row:
-// lane l reads x[(l % 32) * stride + 8 * (l / 32) .. + 7].
-__device__ __forceinline__ bf16x8 lds_operand(const bf16* x, int stride, int lane) {
-  return *reinterpret_cast<const bf16x8*>(x + (lane & 31) * stride + 8 * (lane >> 5));
-}
-
-// A/B operand that contracts over the ROWS of a row-major LDS tile x (16 rows
-// of one contraction step, 32 columns of the output): lane l receives
-// x[sigma(8 * (l / 32) + e) * stride + (l % 32)], e = 0..7, via two
-// ds_read_b64_tr_b16.  Within a 16-lane group, lanes 4r..4r+3 supply the four
-// 8-byte pieces of row r of a 4 x 16 block and lane i receives column i.
-__device__ __forceinline__ bf16x8 lds_operand_tr(const bf16* x, int stride, int lane) {
-  const int g = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
-  const bf16* p0 = x + (4 * (g >> 1) + r) * stride + 16 * (g & 1) + 4 * c;
-  const bf16* p1 = p0 + 8 * stride;
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
-  bf16x8 out;
-  const bf16x4 lo_b = __builtin_bit_cast(bf16x4, lo);
-  const bf16x4 hi_b = __builtin_bit_cast(bf16x4, hi);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    out[e] = lo_b[e];
-    out[4 + e] = hi_b[e];
-  }
-  return out;
-}
-
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Buffer resource over one (batch, head) slab of a (B, T, H, D) tensor: T rows
@@ -166,39 +122,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
 }
 
-// The same slab seen from row r0 on: rows r0 .. T - 1 of the slab are rows
-// 0 .. T - 1 - r0 of the resource and everything past them (and any r0 >= T)
-// reads as zeros.  Tile copies use this so that their per-lane offsets do not
-// depend on the tile.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc_from(const bf16* base, int64_t st, int T, int D, int r0) {
-  const int64_t extent = (int64_t)(T - 1 - r0) * st * 2 + 2 * D;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)r0 * st), (short)0, extent > 0 ? (int)extent : 0,
-                                           0x00020000);
-}
-
-// 16 bytes of one row at element column `col` through a slab resource.
-__device__ __forceinline__ bf16x8 slab_load(__amdgpu_buffer_rsrc_t rs, int row, int st2, int col) {
-  typedef __attribute__((ext_vector_type(4))) int i32x4;
-  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, row * st2 + col * 2, 0, 0);
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-// One LDS DMA instruction: `bytes` (16 or 4) per lane from the buffer at byte
-// offset voff into lds + bytes * lane (lane placement checked on the MI355X).
-// Issued as inline asm on purpose: the compiler then does not track these LDS
-// writes, so it inserts no conservative vmcnt waits before unrelated LDS
-// reads; every wait for them is explicit (dma_barrier).  Vector-memory loads
-// complete in issue order, so the compiler's own waits for its loads can only
-// over-wait.
-template <int bytes>
-__device__ __forceinline__ void lds_dma(__amdgpu_buffer_rsrc_t rs, const void* lds, int voff) {
-  const unsigned ldsaddr = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void*)lds);
-  if constexpr (bytes == 16)
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
-  else
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
-}
-
 // LDS byte address of a __shared__ location (taken once per kernel; the
 // per-tile addresses are then plain 32-bit offsets from it, so the loops carry
 // no generic-to-LDS pointer conversions).
@@ -206,7 +129,13 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const lds_void*)p);
 }
 
-// As lds_dma, to an LDS byte address.
+// One LDS DMA instruction: `bytes` (16 or 4) per lane from the buffer at byte
+// offset voff into LDS byte address ldsaddr + bytes * lane (lane placement
+// checked on the MI355X).  Issued as inline asm on purpose: the compiler then
+// does not track these LDS writes, so it inserts no conservative vmcnt waits
+// before unrelated LDS reads; every wait for them is explicit (dma_barrier,
+// vm_wait_upto).  Vector-memory loads complete in issue order, so the
+// compiler's own waits for its loads can only over-wait.
 template <int bytes>
 __device__ __forceinline__ void lds_dma_at(__amdgpu_buffer_rsrc_t rs, unsigned ldsaddr, int voff) {
   if constexpr (bytes == 16)
@@ -235,129 +164,6 @@ struct SlabCursor {
 // elements, positioned at row r0.
 __device__ __forceinline__ SlabCursor slab_cursor(const bf16* base, int64_t st, int T, int D, int r0) {
   return {(uint64_t)(uintptr_t)(base + (int64_t)r0 * st), (int64_t)(T - 1 - r0) * st * 2 + 2 * D};
-}
-
-// Direct buffer -> LDS copies of a ROWS x D tile starting at row r0 (st2 = row
-// stride in bytes).  Each instruction moves 1 KB, and a layout is chosen by
-// choosing each lane's source address.  The NW waves of a workgroup split the
-// 1 KB pieces among themselves; nothing passes through VGPRs.
-//
-// Row-major: rows are contiguous (2*D bytes each), for ds_read_b64_tr_b16.
-template <int ROWS, int D, int NW>
-__device__ __forceinline__ void dma_rows(__amdgpu_buffer_rsrc_t rs, int st2, int r0, bf16* lds, int wave, int lane) {
-  constexpr int NI = ROWS * D / 512, LPR = D / 8;  // 1 KB pieces; lanes per row
-  static_assert(NI % NW == 0, "tile must split evenly over the waves");
-#pragma unroll
-  for (int i = 0; i < NI / NW; ++i) {
-    const int j = wave + NW * i;
-    const int row = r0 + j * (64 / LPR) + lane / LPR;
-    lds_dma<16>(rs, lds + j * 512, row * st2 + (lane % LPR) * 16);
-  }
-}
-
-// Fragment-major: piece f = rb * (D / 16) + s holds, in lane order l, the
-// 16 bytes of row 32 rb + l % 32 at columns 16 s + 8 (l / 32) .. + 7 -- exactly
-// the A/B operand of one 32x32x16 MFMA -- so an operand read is one contiguous
-// 1 KB ds_read_b128 (frag_operand).
-template <int ROWS, int D, int NW>
-__device__ __forceinline__ void dma_frags(__amdgpu_buffer_rsrc_t rs, int st2, int r0, bf16* lds, int wave, int lane) {
-  constexpr int NI = ROWS * D / 512, SPR = D / 16;  // 1 KB pieces; pieces per 32-row block
-  static_assert(NI % NW == 0, "tile must split evenly over the waves");
-#pragma unroll
-  for (int i = 0; i < NI / NW; ++i) {
-    const int j = wave + NW * i;
-    const int row = r0 + 32 * (j / SPR) + (lane & 31);
-    const int col = 16 * (j % SPR) + 8 * (lane >> 5);
-    lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
-  }
-}
-
-// Swizzled fragment layout: one LDS copy of a ROWS x D tile that serves both
-// operand orientations without bank conflicts.  Piece f = rb * (D / 16) + s
-// (1 KB) holds rows 32 rb .. 32 rb + 31, columns 16 s .. 16 s + 15, as 64
-// chunks of 16 bytes; chunk p holds half h = p / 32 (columns 16 s + 8 h ..
-// + 7) of row 32 rb + ((p % 32) ^ 4 h).
-//  * An MFMA operand along the rows (lane l: row l % 32, half l / 32) is one
-//    ds_read_b128 per lane; each group of 16 lanes covers 16 distinct chunk
-//    slots mod 256 bytes.
-//  * A transposed operand (ds_read_b64_tr_b16, 4 rows x both halves per
-//    16-lane group) touches 8 chunks whose slots differ mod 256 bytes, because
-//    the XOR moves the second half of rows 4 m .. 4 m + 3 by 4 slots.
-__device__ __forceinline__ int swz_chunk(int row, int h) { return 32 * h + ((row & 31) ^ (4 * h)); }
-
-template <int ROWS, int D, int NW>
-__device__ __forceinline__ void dma_swz(__amdgpu_buffer_rsrc_t rs, int st2, bf16* lds, int wave, int lane) {
-  constexpr int NI = ROWS * D / 512, SPR = D / 16;  // 1 KB pieces; pieces per 32-row block
-  static_assert(NI % NW == 0, "tile must split evenly over the waves");
-  const int h = lane >> 5, r = (lane & 31) ^ (4 * h);
-#pragma unroll
-  for (int i = 0; i < NI / NW; ++i) {
-    const int j = wave + NW * i;
-    const int row = 32 * (j / SPR) + r;
-    const int col = 16 * (j % SPR) + 8 * h;
-    lds_dma<16>(rs, lds + j * 512, row * st2 + col * 2);
-  }
-}
-
-// dma_swz to the LDS byte address `lds` with the per-lane source offsets
-// precomputed by swz_offsets (they depend only on the lane and the row stride).
-template <int ROWS, int D, int NW>
-struct SwzOffsets {
-  int v[ROWS * D / 512 / NW];
-};
-template <int ROWS, int D, int NW>
-__device__ __forceinline__ SwzOffsets<ROWS, D, NW> swz_offsets(int st2, int wave, int lane) {
-  constexpr int NI = ROWS * D / 512, SPR = D / 16;
-  static_assert(NI % NW == 0, "tile must split evenly over the waves");
-  SwzOffsets<ROWS, D, NW> o;
-  const int h = lane >> 5, r = (lane & 31) ^ (4 * h);
-#pragma unroll
-  for (int i = 0; i < NI / NW; ++i) {
-    const int j = wave + NW * i;
-    o.v[i] = (32 * (j / SPR) + r) * st2 + (16 * (j % SPR) + 8 * h) * 2;
-  }
-  return o;
-}
-template <int ROWS, int D, int NW>
-__device__ __forceinline__ void dma_swz_at(__amdgpu_buffer_rsrc_t rs, const SwzOffsets<ROWS, D, NW>& o, unsigned lds,
-                                           int wave) {
-  constexpr int NI = ROWS * D / 512;
-#pragma unroll
-  for (int i = 0; i < NI / NW; ++i) lds_dma_at<16>(rs, lds + (wave + NW * i) * 1024, o.v[i]);
-}
-
-// Operand (rb, s) along the rows of a swizzled tile: lane l gets row
-// 32 rb + l % 32, columns 16 s + 8 (l / 32) .. + 7.
-template <int D>
-__device__ __forceinline__ bf16x8 swz_operand(const bf16* lds, int rb, int s, int lane) {
-  const int h = lane >> 5;
-  return *reinterpret_cast<const bf16x8*>(lds + (rb * (D / 16) + s) * 512 + swz_chunk(lane & 31, h) * 8);
-}
-
-// Transposed operand of a swizzled tile, contracting over 16 rows r0 ..
-// r0 + 15 (r0 a multiple of 16) for the 32 columns c0 .. c0 + 31 (c0 a
-// multiple of 32): the same values and order as lds_operand_tr on a
-// row-major copy.
-template <int D>
-__device__ __forceinline__ bf16x8 swz_operand_tr(const bf16* lds, int r0, int c0, int lane) {
-  const int g = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
-  const int row = r0 + 4 * (g >> 1) + r;
-  const int s = c0 / 16 + (g & 1), h = c >> 1;
-  const bf16* base = lds + ((row >> 5) * (D / 16) + s) * 512 + 4 * (c & 1);
-  const bf16* p0 = base + swz_chunk(row, h) * 8;
-  const bf16* p1 = base + swz_chunk(row + 8, h) * 8;
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
-  bf16x8 out;
-  const bf16x4 lo_b = __builtin_bit_cast(bf16x4, lo);
-  const bf16x4 hi_b = __builtin_bit_cast(bf16x4, hi);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    out[e] = lo_b[e];
-    out[4 + e] = hi_b[e];
-  }
-  return out;
 }
 
 // Barrier for tiles that arrive by LDS DMA: wait until at most `pending` of
@@ -413,7 +219,6 @@ __device__ __forceinline__ void vm_wait_upto(int newer) {
 // Ordinary (compiler-tracked) buffer loads at a byte offset; reads past the
 // resource's extent return zeros.
 __device__ __forceinline__ bf16x8 buf_load_b128(__amdgpu_buffer_rsrc_t rs, int voff) {
-  typedef __attribute__((ext_vector_type(4))) int i32x4;
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0));
 }
 __device__ __forceinline__ float buf_load_b32(__amdgpu_buffer_rsrc_t rs, int voff) {
@@ -515,50 +320,6 @@ __device__ __forceinline__ bf16x8 lds_read_b128(unsigned addr) {
 __device__ __forceinline__ void lds_write_b64(unsigned addr, bf16x4 v) {
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
   *(lds_bf16x4*)(uintptr_t)addr = v;
-}
-
-// Waits for every outstanding vector-memory op of this wave.  Used once after
-// a kernel's prologue loads (and stores), so that inside the DMA-pipelined
-// loop the compiler has nothing of its own left to wait for and dma_barrier's
-// counts cover exactly the DMA of newer tiles.
-__device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
-
-// Operand (rb, s) of a fragment-major tile.
-template <int D>
-__device__ __forceinline__ bf16x8 frag_operand(const bf16* lds, int rb, int s, int lane) {
-  return *reinterpret_cast<const bf16x8*>(lds + (rb * (D / 16) + s) * 512 + lane * 8);
-}
-
-// Workgroups of a persistent launch: as many as the device holds at once
-// (occupancy x compute units), at most n_items, rounded down to a multiple of 8
-// (the XCD count) when that is at least 8.  Cached per kernel and device.
-inline int persistent_grid(const void* kernel, int block, int64_t n_items) {
-  struct Entry {
-    const void* kernel;
-    int device, grid;
-  };
-  static std::mutex mu;
-  static Entry cache[64];
-  static int n_cache = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  int full = 0;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < n_cache; ++i)
-      if (cache[i].kernel == kernel && cache[i].device == dev) full = cache[i].grid;
-  }
-  if (full == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu < 1) per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-    full = per_cu * cus;
-    std::lock_guard<std::mutex> lock(mu);
-    if (n_cache < 64) cache[n_cache++] = {kernel, dev, full};
-  }
-  int64_t g = n_items < full ? n_items : full;
-  if (g >= 8) g &= ~(int64_t)7;
-  return (int)(g > 0 ? g : 1);
 }
 
 }  // namespace hlm
