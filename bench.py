@@ -14,7 +14,12 @@ MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
 (HIP-event timed on the launch stream) and the CPU baseline: the reference's
 `torch` backend restated on the host CPU (configs[0] shape, fp32, forward).
 
-  python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline]
+Steps are eager launches by default (they run ahead of the GPU); --graph times
+HIP-graph replays of one captured step instead (the way a training step runs
+under torch.compile's CUDA-graph mode).  The default warmup (300 steps) lets
+the GPU reach its steady clock before timing starts.
+
+  python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline] [--graph]
 """
 from __future__ import annotations
 
@@ -45,6 +50,7 @@ CONFIGS = {
     "cfg5_long": dict(B=1, T=16384, H=16, D=128, W=2048),
 }
 CPU_CONFIG = dict(B=2, T=1024, H=6, D=64, W=256)
+KERNEL_NAMES = {"fwd": "attn_fwd_kernel", "bwd_dq": "attn_bwd_dq_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel"}
 
 
 def pairs(T: int, W: int | None) -> int:
@@ -93,8 +99,13 @@ class Problem:
         self.s = {n: st(getattr(self, n)) for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
         self.window = 0 if cfg["W"] is None else cfg["W"]
         self.scale = 1.0 / math.sqrt(D)
-        self.stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        self.device = device
         self.dims = (B, T, H, H, D)
+
+    @property
+    def stream(self):
+        # torch's current stream at call time (a capture stream inside graph capture)
+        return ctypes.c_void_p(self.torch.cuda.current_stream(self.device).cuda_stream)
 
     def fwd(self):
         rc = self.lib.hlm_attn_fwd(
@@ -139,17 +150,46 @@ def event_time_ms(torch, fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def measure(name: str, steps: int, warmup: int, device) -> dict:
+def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> dict:
+    """Times `steps` fwd+bwd steps after `warmup` untimed ones.  By default the
+    steps are eager launches from Python (the launches run ahead of the GPU,
+    so this is GPU time); with graph=True one step (its three kernel launches)
+    is captured once in a HIP graph and replayed per step, as a training step
+    under torch.compile's CUDA-graph mode runs it."""
     import torch
 
     cfg = CONFIGS[name]
     prob = Problem(cfg, seed=0, device=device)
+
+    def eager_wall(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            prob.step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
     for _ in range(warmup):
         prob.step()
+    eager_ms = eager_wall(steps)
+    run_step = prob.step
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            prob.step()  # one eager step on the capture stream before capture
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            prob.step()
+        run_step = g.replay
+        for _ in range(warmup):
+            run_step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        prob.step()
+        run_step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
 
@@ -160,16 +200,19 @@ def measure(name: str, steps: int, warmup: int, device) -> dict:
         "bwd_dkdv": event_time_ms(torch, prob.bwd_dkdv, reps),
     }
     bwd_ms = event_time_ms(torch, prob.bwd, reps)
-    step_ms = event_time_ms(torch, prob.step, reps)
+    step_ms = event_time_ms(torch, run_step, reps)
     fl = effective_flops(cfg)
     by = algorithmic_bytes(cfg)
     total = fl["fwd"] + fl["bwd"]
     dominant = max(kern, key=kern.get)
+    kernel_name = KERNEL_NAMES[dominant]
     achieved = fl[dominant] / (kern[dominant] * 1e-3) / 1e12
     return {
         "cfg": cfg,
         "wall_ms_per_step": wall_ms,
         "event_ms_per_step": step_ms,
+        "eager_wall_ms_per_step": eager_ms,
+        "graph": graph,
         "fwd_ms": kern["fwd"],
         "bwd_ms": bwd_ms,
         "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
@@ -183,7 +226,7 @@ def measure(name: str, steps: int, warmup: int, device) -> dict:
         "dominant": dominant,
         "roofline": {
             "bound": "mfma",
-            "kernel": {"fwd": "attn_fwd_kernel", "bwd_dq": "attn_bwd_dq_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel"}[dominant],
+            "kernel": kernel_name,
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
@@ -191,7 +234,13 @@ def measure(name: str, steps: int, warmup: int, device) -> dict:
             "algorithmic_flops_per_launch": fl[dominant],
             "algorithmic_bytes_per_launch": by[dominant],
             "launch_us": round(kern[dominant] * 1e3, 2),
-            "traffic": read_traffic(name, dominant),
+            "traffic": read_traffic(name, kernel_name),
+            # The same launch against the HBM roofline (algorithmic bytes / launch time).
+            "hbm": {
+                "achieved_GBs": round(by[dominant] / (kern[dominant] * 1e-3) / 1e9, 1),
+                "peak_GBs": PEAK_HBM_GBS,
+                "frac": round(by[dominant] / (kern[dominant] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            },
         },
     }
 
@@ -258,11 +307,14 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # The GPU needs ~20 ms of work after idling before it runs at full speed
+    # (the first 100 steps run ~12% slower); 300 steps is ~50 ms.
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", default="cfg2_local", choices=sorted(CONFIGS))
     ap.add_argument("--sweep", action="store_true", help="also time every config (printed to stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step instead of eager launches")
     ap.add_argument(
         "--copy-mib", type=int, default=0,
         help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
@@ -287,7 +339,7 @@ def main() -> int:
 
     if args.sweep:
         for name in CONFIGS:
-            r = measure(name, max(10, args.steps // 2), args.warmup, device)
+            r = measure(name, max(10, args.steps // 2), args.warmup, device, graph=args.graph)
             print(
                 f"{name}: fwd {r['fwd_ms']*1e3:.1f} us ({r['tflops']['fwd']:.0f} TF) | "
                 f"bwd {r['bwd_ms']*1e3:.1f} us ({r['tflops']['bwd']:.0f} TF) | "
@@ -297,7 +349,7 @@ def main() -> int:
                 flush=True,
             )
 
-    r = measure(args.config, args.steps, args.warmup, device)
+    r = measure(args.config, args.steps, args.warmup, device, graph=args.graph)
     cfg = r["cfg"]
     w = "causal" if cfg["W"] is None else f"window={cfg['W']}"
     line = {
@@ -331,6 +383,11 @@ def main() -> int:
         },
         "tflops": {k: round(v, 2) for k, v in r["tflops"].items()},
         "kernel_us": r["kernel_us"],
+        "timing": {
+            "step": "HIP-graph replay of one fwd+bwd step" if r["graph"] else "eager launches from Python",
+            "eager_wall_ms_per_step": round(r["eager_wall_ms_per_step"], 5),
+            "event_ms_per_step": round(r["event_ms_per_step"], 5),
+        },
         "roofline": r["roofline"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
