@@ -73,7 +73,7 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 // vector-memory counter counts tile copies only.
 // ---------------------------------------------------------------------------
 template <int D, int NBUF, int PRE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdArgs a) {
   using L = CS<D>;
   constexpr int NW = 4, BM = NW * 32, BN = 32;
   constexpr int NDB = D / 32, NS = D / 16;
@@ -199,6 +199,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
 
   const bool wave_live = qw0 < T;
   const int wq_hi = min(qw0 + 31, T - 1);
+  // D = 64 issues all S and dP operand reads of a tile at once (the registers
+  // for that fit with 3 waves per SIMD); D = 128 reads them as it goes.
+  constexpr bool kBatchReads = D == 64;
+  [[maybe_unused]] const f32x16 slse = splat16(nlse2), sdel = splat16(ndelta);
 
   int issued_hi = n_pre - 1;
   for (int it = 0; it < n_tiles; ++it) {
@@ -214,29 +218,77 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(BwdArgs a) {
     const int k0 = (t_lo + it) * BN;
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
-    f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
-    if (!full) {
-      // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
-      const int d0 = myq - k0 - 4 * h32;
+    if constexpr (kBatchReads) {
+      // All operand reads of S and dP are issued before the first MFMA.
+      bf16x8 kop[NS], vop[NS];
+      // off_s[s] == off_s[0] ^ 32 s (the swizzle permutes 16-byte units within a
+      // row, and unit 2 s + h32 differs from unit h32 in bits 1.. only).
+      int ob = off_s[0], tb = tro[0][0];
+      asm volatile("" : "+v"(ob), "+v"(tb));
 #pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const int cst = 8 * (x >> 2) + (x & 3);
-        sacc[x] = (unsigned)(d0 - cst) < (unsigned)W ? sacc[x] : -INFINITY;
+      for (int s = 0; s < NS; ++s) {
+        kop[s] = cs_operand<D>(kt, ob ^ (32 * s), 0);
+        vop[s] = cs_operand<D>(vt, ob ^ (32 * s), 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 sacc;
+      if (full) {
+        sacc = mfma32(kop[0], qreg[0], slse);
+      } else {
+        // Column c = 4 h32 + 8 (x / 4) + x % 4 of the tile is key k0 + c; it is
+        // visible to row myq iff d0 - W < c <= d0 with d0 = myq - k0 - 4 h32.
+        const int d0 = myq - k0 - 4 * h32;
+        const int lo = d0 - W + 1;
+        const unsigned vhi = d0 < 0 ? 0u : d0 >= 31 ? ~0u : (2u << d0) - 1u;
+        const unsigned vlo = lo <= 0 ? ~0u : lo >= 32 ? 0u : ~0u << lo;
+        const unsigned vis = vhi & vlo;
+        f32x16 st = slse;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          const int cst = 8 * (x >> 2) + (x & 3);
+          st[x] = ((vis >> cst) & 1u) ? st[x] : -INFINITY;
+        }
+        sacc = mfma32(kop[0], qreg[0], st);
+      }
+      f32x16 pacc = mfma32(vop[0], doreg[0], sdel);
+#pragma unroll
+      for (int s = 1; s < NS; ++s) {
+        sacc = mfma32(kop[s], qreg[s], sacc);
+        pacc = mfma32(vop[s], doreg[s], pacc);
+      }
+      bf16x8 dsb[2];
+#pragma unroll
+      for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dqacc[db] = mfma32(cs_operand_tr<D>(kt, cs_tr_off_from<D>(tb, db, 0), cs_tr_off_from<D>(tb, db, 1), 16 * kk), dsb[kk], dqacc[db]);
+    } else {
+      f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
+      if (!full) {
+        // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
+        const int d0 = myq - k0 - 4 * h32;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          const int cst = 8 * (x >> 2) + (x & 3);
+          sacc[x] = (unsigned)(d0 - cst) < (unsigned)W ? sacc[x] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        sacc = mfma32(cs_operand<D>(kt, off_s[s], 0), qreg[s], sacc);
+        pacc = mfma32(cs_operand<D>(vt, off_s[s], 0), doreg[s], pacc);
+      }
+      bf16x8 dsb[2];
+#pragma unroll
+      for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
     }
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      sacc = mfma32(cs_operand<D>(kt, off_s[s], 0), qreg[s], sacc);
-      pacc = mfma32(cs_operand<D>(vt, off_s[s], 0), doreg[s], pacc);
-    }
-    bf16x8 dsb[2];
-#pragma unroll
-    for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-        dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
   }
 
   // dQ through LDS: every wave is past its last tile, so wave w may use the

@@ -291,6 +291,15 @@ __device__ __forceinline__ int cs_tr_off(int db, int second, int lane) {
   return CS<D>::byte(row, col >> 3) + 8 * ((col >> 2) & 1);
 }
 
+// cs_tr_off(db, second, lane) from cs_tr_off(0, 0, lane): column block db
+// flips bit 2 of the 16-byte unit (byte ^ 64 db); the second 8 rows add one
+// (D = 64) or two (D = 128) 1 KB chunks and flip bit 1 of the swizzle
+// (byte ^ 32), and neither touches bits the base offset has set.
+template <int D>
+__device__ __forceinline__ int cs_tr_off_from(int t0, int db, int second) {
+  return t0 ^ (64 * db) ^ (second ? ((D == 64 ? 1024 : 2048) | 32) : 0);
+}
+
 // Transposed operand of a cs tile, contracting over the 16 rows r0 .. r0 + 15
 // (r0 a multiple of 16) for 32 columns: lane l receives the values of column
 // l % 32 at rows sigma(8 (l / 32) + e) (the order of lds_operand_tr).  o0, o1 =
