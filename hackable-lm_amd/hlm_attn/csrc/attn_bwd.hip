@@ -138,8 +138,8 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
     kof[i] = L::dma_row(j, lane) * sk2 + L::dma_col_bytes(j, lane);
     vof[i] = L::dma_row(j, lane) * sv2 + L::dma_col_bytes(j, lane);
   }
-  auto load_tile = [&](int t) __attribute__((always_inline)) {
-    const unsigned slot = lring + (unsigned)(t % NBUF) * SLOTB;
+  // Copies tile t into the ring slot at LDS address `slot`.
+  auto load_tile_at = [&](int t, unsigned slot) __attribute__((always_inline)) {
     const int kb = (t_lo + t) * BN * sk2, vb = (t_lo + t) * BN * sv2;
 #pragma unroll
     for (int i = 0; i < CPT / NW; ++i) {
@@ -148,6 +148,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
       lds_dma_at<16>(rv, slot + TILEB + piece, vb + vof[i]);
     }
   };
+  auto load_tile = [&](int t) __attribute__((always_inline)) { load_tile_at(t, lring + (unsigned)(t % NBUF) * SLOTB); };
   const int n_pre = min(PRE, n_tiles);
   for (int t = 0; t < n_pre; ++t) load_tile(t);
 
@@ -205,18 +206,30 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   [[maybe_unused]] const f32x16 slse = splat16(nlse2), sdel = splat16(ndelta);
 
   int issued_hi = n_pre - 1;
+  unsigned kt = lring;  // ring slot of tile it
   for (int it = 0; it < n_tiles; ++it) {
     // Wait for this wave's copies of tile it (newer tiles may stay in flight);
     // the barrier makes every wave's copies visible and frees the slot of tile
     // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
-    // NBUF - 1 tiles ahead.
-    dma_barrier_upto<PER, NBUF - 1>(issued_hi - it);
-    const int want = min(it + NBUF - 1, n_tiles - 1);
-    while (issued_hi < want) load_tile(++issued_hi);
-
-    const unsigned kt = lring + (unsigned)(it % NBUF) * SLOTB, vt = kt + TILEB;
+    // NBUF - 1 tiles ahead.  In the steady state (1 <= it <= n_tiles - NBUF)
+    // exactly NBUF - 2 tiles are in flight behind tile it and one tile is
+    // copied, into the slot just freed: no counting branches.
+    const unsigned kprev = kt == lring ? lring + (NBUF - 1) * SLOTB : kt - SLOTB;
+    if (it >= 1 && it + NBUF - 1 <= n_tiles - 1) {
+      dma_barrier<(NBUF - 2) * PER>();
+      load_tile_at(++issued_hi, kprev);
+    } else {
+      dma_barrier_upto<PER, NBUF - 1>(issued_hi - it);
+      const int want = min(it + NBUF - 1, n_tiles - 1);
+      while (issued_hi < want) load_tile(++issued_hi);
+    }
+    const unsigned vt = kt + TILEB;
+    const unsigned knext = kt == lring + (NBUF - 1) * SLOTB ? lring : kt + SLOTB;
     const int k0 = (t_lo + it) * BN;
-    if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
+    if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) {
+      kt = knext;
+      continue;
+    }
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
     if constexpr (kBatchReads) {
       // All operand reads of S and dP are issued before the first MFMA.
@@ -238,10 +251,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
         // Column c = 4 h32 + 8 (x / 4) + x % 4 of the tile is key k0 + c; it is
         // visible to row myq iff d0 - W < c <= d0 with d0 = myq - k0 - 4 h32.
         const int d0 = myq - k0 - 4 * h32;
-        const int lo = d0 - W + 1;
-        const unsigned vhi = d0 < 0 ? 0u : d0 >= 31 ? ~0u : (2u << d0) - 1u;
-        const unsigned vlo = lo <= 0 ? ~0u : lo >= 32 ? 0u : ~0u << lo;
-        const unsigned vis = vhi & vlo;
+        const unsigned vis = band_bits(d0 - W + 1, d0);
         f32x16 st = slse;
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
@@ -289,6 +299,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
         for (int db = 0; db < NDB; ++db)
           dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
     }
+    kt = knext;
   }
 
   // dQ through LDS: every wave is past its last tile, so wave w may use the

@@ -291,6 +291,15 @@ __device__ __forceinline__ int cs_tr_off(int db, int second, int lane) {
   return CS<D>::byte(row, col >> 3) + 8 * ((col >> 2) & 1);
 }
 
+// Bit c (0 <= c < 32) set iff lo <= c <= hi: the columns of a 32-wide score
+// block that a row can see, as one register (masks then cost a bit test per
+// element and no per-element constants).
+__device__ __forceinline__ unsigned band_bits(int lo, int hi) {
+  const unsigned vhi = hi < 0 ? 0u : hi >= 31 ? ~0u : (2u << hi) - 1u;
+  const unsigned vlo = lo <= 0 ? ~0u : lo >= 32 ? 0u : ~0u << lo;
+  return vhi & vlo;
+}
+
 // cs_tr_off(db, second, lane) from cs_tr_off(0, 0, lane): column block db
 // flips bit 2 of the 16-byte unit (byte ^ 64 db); the second 8 rows add one
 // (D = 64) or two (D = 128) 1 KB chunks and flip bit 1 of the swizzle
