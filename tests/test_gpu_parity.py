@@ -102,6 +102,45 @@ def test_fwd_bwd_matches_oracle(B, T, H, Hkv, D, window, seed):
     assert_grad("dv", dv, rdv)
 
 
+# Shapes around the kernels' tile and ring boundaries: 32-row query blocks,
+# 128-row workgroup tiles, 32/64-key tiles and ring depths of 2-6 tiles
+# (T and W one below, at and one above those multiples), both head sizes,
+# MHA and MQA.
+EDGE_CASES = [
+    # B, T, H, Hkv, D, window
+    (1, 31, 2, 2, 64, None),
+    (1, 33, 2, 1, 64, 32),
+    (1, 95, 2, 2, 64, 33),
+    (1, 97, 2, 2, 128, 64),
+    (1, 129, 2, 2, 64, 63),
+    (1, 160, 2, 1, 64, 65),
+    (1, 191, 2, 2, 128, 127),
+    (1, 193, 2, 2, 64, 128),
+    (1, 255, 2, 2, 64, 129),
+    (1, 257, 2, 1, 128, 191),
+    (1, 256, 3, 3, 64, 192),
+    (2, 385, 2, 2, 64, 200),
+    (1, 640, 2, 2, 64, 320),
+    (1, 700, 2, 2, 128, 512),
+]
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D,window", EDGE_CASES)
+def test_tile_edge_shapes_match_oracle(B, T, H, Hkv, D, window):
+    dev = _device()
+    seed = 100 + T
+    print(f"case B={B} T={T} H={H} Hkv={Hkv} D={D} W={window} seed={seed}", flush=True)
+    q, k, v, do = make_inputs(B, T, H, Hkv, D, seed)
+    o, lse, dq, dk, dv = run_hip(q, k, v, do, window, dev)
+    ro, rlse = oracle.forward(q, k, v, window)
+    rdq, rdk, rdv = oracle.backward(q, k, v, do, window)
+    assert_out("o", o, ro)
+    assert_lse(lse, rlse)
+    assert_grad("dq", dq, rdq)
+    assert_grad("dk", dk, rdk)
+    assert_grad("dv", dv, rdv)
+
+
 FULL_CONFIGS = [
     # name, B, T, H, D, window  (BASELINE.json configs[1..4]; cfg4 = one local and one full layer)
     ("cfg2_local", 8, 2048, 12, 64, 512),
