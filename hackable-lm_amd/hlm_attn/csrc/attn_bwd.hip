@@ -205,23 +205,37 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   constexpr bool kBatchReads = D == 64;
   [[maybe_unused]] const f32x16 slse = splat16(nlse2), sdel = splat16(ndelta);
 
+  // D = 64 synchronises every second tile (tiles it and it + 1 behind one
+  // barrier); D = 128, whose staging leaves only one tile in flight at the
+  // start, every tile.
+  constexpr int KG = D == 64 ? 2 : 1;
+  static_assert(PRE >= KG && NBUF >= 2 * KG + 1, "the first group is in flight before the loop");
   int issued_hi = n_pre - 1;
   unsigned kt = lring;  // ring slot of tile it
   for (int it = 0; it < n_tiles; ++it) {
-    // Wait for this wave's copies of tile it (newer tiles may stay in flight);
-    // the barrier makes every wave's copies visible and frees the slot of tile
-    // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
-    // NBUF - 1 tiles ahead.  In the steady state (1 <= it <= n_tiles - NBUF)
-    // exactly NBUF - 2 tiles are in flight behind tile it and one tile is
-    // copied, into the slot just freed: no counting branches.
-    const unsigned kprev = kt == lring ? lring + (NBUF - 1) * SLOTB : kt - SLOTB;
-    if (it >= 1 && it + NBUF - 1 <= n_tiles - 1) {
-      dma_barrier<(NBUF - 2) * PER>();
-      load_tile_at(++issued_hi, kprev);
-    } else {
-      dma_barrier_upto<PER, NBUF - 1>(issued_hi - it);
-      const int want = min(it + NBUF - 1, n_tiles - 1);
-      while (issued_hi < want) load_tile(++issued_hi);
+    // At the first tile of each group: wait for this wave's copies of the
+    // group (newer tiles may stay in flight); the barrier makes every wave's
+    // copies visible and frees the slots of the previous group (and, at it =
+    // 0, the staging area); then the ring is topped up to NBUF - 1 tiles past
+    // it.  In the steady state (KG <= it <= n_tiles - NBUF) exactly NBUF - 2 KG
+    // tiles are in flight behind the group and KG tiles are copied, into the
+    // slots just freed: no counting branches.
+    if (it % KG == 0) {
+      if (it >= KG && it + NBUF - 1 <= n_tiles - 1) {
+        dma_barrier<(NBUF - 2 * KG) * PER>();
+        unsigned ks = kt;
+#pragma unroll
+        for (int m = 0; m < KG; ++m) ks = ks == lring ? lring + (NBUF - 1) * SLOTB : ks - SLOTB;
+#pragma unroll
+        for (int m = 0; m < KG; ++m) {  // slots of tiles it - KG .. it - 1
+          load_tile_at(++issued_hi, ks);
+          ks = ks == lring + (NBUF - 1) * SLOTB ? lring : ks + SLOTB;
+        }
+      } else {
+        dma_barrier_upto<PER, NBUF - 1>(issued_hi - min(it + KG - 1, n_tiles - 1));
+        const int want = min(it + NBUF - 1, n_tiles - 1);
+        while (issued_hi < want) load_tile(++issued_hi);
+      }
     }
     const unsigned vt = kt + TILEB;
     const unsigned knext = kt == lring + (NBUF - 1) * SLOTB ? lring : kt + SLOTB;
@@ -365,7 +379,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   constexpr bool STAGE_KV = D == 64;
   static_assert(CPT % NW == 0, "tile chunks split evenly over the waves");
   static_assert(!STAGE_KV || PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
-  static_assert(PRE >= 1 && PRE < NBUF, "tile 0 is in flight before the loop");
+  static_assert(PRE >= 2 && PRE < NBUF, "tiles 0 and 1 are in flight before the loop");
+  static_assert(NBUF >= 4, "a barrier every second tile needs two tiles of slack");
   static_assert(NBUF * (PER + 1) < 64 && 2 * NS + 2 * NCH + PRE * (PER + 1) < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
   __shared__ __attribute__((aligned(256))) float stbuf[NBUF][128];  // [0, 64): -lse * log2(e), [64, 128): -delta
@@ -510,16 +525,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   int cp_t = 0;  // query tile (within the current head) of the compute pointer
 
   for (int it = 0; it < n_iter; ++it) {
-    // Wait for this wave's copies of tile it (newer tiles may stay in flight);
-    // the barrier makes every wave's copies visible and frees the slot of tile
-    // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
-    // NBUF - 1 tiles ahead.
-    if (wave < 2)
-      dma_barrier_upto<PER + 1, NBUF - 1>(issued - 1 - it);
-    else
-      dma_barrier_upto<PER, NBUF - 1>(issued - 1 - it);
-    const int want = min(it + NBUF, n_iter);
-    while (issued < want) load_tile();
+    // Every second tile: wait for this wave's copies of tiles it and it + 1
+    // (newer tiles may stay in flight); the barrier makes every wave's copies
+    // visible and frees the slots of tiles it - 2 and it - 1 (and, at it = 0,
+    // the staging area); then the ring is topped up to NBUF - 1 tiles past
+    // it.  Tile it + 1 then needs no barrier of its own.
+    if ((it & 1) == 0) {
+      const int need = min(it + 1, n_iter - 1);
+      if (wave < 2)
+        dma_barrier_upto<PER + 1, NBUF - 1>(issued - 1 - need);
+      else
+        dma_barrier_upto<PER, NBUF - 1>(issued - 1 - need);
+      const int want = min(it + NBUF, n_iter);
+      while (issued < want) load_tile();
+    }
 
     const int slot = it % NBUF;
     const unsigned qs_t = lring + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
