@@ -13,6 +13,8 @@ count only unmasked (query, key) pairs P(T, W): fwd 4*D*P, bwd 8*D*P per
 MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
 (HIP-event timed on the launch stream) and the CPU baseline: the reference's
 `torch` backend restated on the host CPU (configs[0] shape, fp32, forward).
+A "producer" object times the q/k RMSNorm + partial RoPE kernels that feed
+attention (forward and backward) at cfg2's q/k shape against the HBM roofline.
 
 Steps are eager launches by default (they run ahead of the GPU); --graph times
 HIP-graph replays of one captured step instead (the way a training step runs
@@ -20,6 +22,7 @@ under torch.compile's CUDA-graph mode).  The default warmup (300 steps) lets
 the GPU reach its steady clock before timing starts.
 
   python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline] [--graph]
+                  [--no-producer]
 """
 from __future__ import annotations
 
@@ -135,6 +138,109 @@ class Problem:
     def step(self):
         self.fwd()
         self.bwd()
+
+
+PRODUCER_CONFIG = dict(B=8, T=2048, H=12, Hkv=12, D=64, R=16)  # cfg2's q/k, model.py's R = D / 4
+PRODUCER_SETS = 4  # buffer sets rotated per launch: 4 x 176 MB exceeds the 256 MB last-level cache
+
+
+def producer_bytes(cfg: dict) -> dict:
+    """Compulsory HBM bytes per launch of the q/k RMSNorm + RoPE producer:
+    forward reads q, k and the bf16 cos / sin tables and writes q, k (bf16);
+    backward also reads the two incoming gradients."""
+    n = cfg["B"] * cfg["T"] * (cfg["H"] + cfg["Hkv"]) * cfg["D"] * 2  # one bf16 pass over q and k
+    tables = 2 * cfg["T"] * cfg["R"] * 2
+    return {"fwd": 2 * n + tables, "bwd": 3 * n + tables}
+
+
+class ProducerProblem:
+    """q / k as strided views of fused (B, T, (H + 2 Hkv) D) projections, as
+    model.py:92-99 makes them, fp32 (T, R) tables, and preallocated outputs;
+    PRODUCER_SETS independent sets so that consecutive launches touch
+    different memory."""
+
+    def __init__(self, cfg: dict, seed: int, device, sets: int = PRODUCER_SETS):
+        import torch
+        from hlm_attn import _lib
+
+        self.torch, self.lib, self.cfg, self.device = torch, _lib.load(), cfg, device
+        B, T, H, Hkv, D, R = (cfg[k] for k in ("B", "T", "H", "Hkv", "D", "R"))
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        # bf16 tables, as RotaryEmbedding hands them to the producer (model.py:62-70)
+        ang = torch.rand(T, R // 2, generator=g) * 6.0
+        self.cos = torch.cat((ang.cos(), ang.cos()), -1).to(torch.bfloat16).to(device)
+        self.sin = torch.cat((ang.sin(), ang.sin()), -1).to(torch.bfloat16).to(device)
+        self.table_dtype = _lib.TABLE_BF16
+        self.sets = []
+        for _ in range(sets):
+            qkv = torch.randn(B, T, (H + 2 * Hkv) * D, generator=g).to(torch.bfloat16).to(device)
+            q = qkv[..., : H * D].view(B, T, H, D)
+            k = qkv[..., H * D : (H + Hkv) * D].view(B, T, Hkv, D)
+            gq = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)
+            gk = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16).to(device)
+            out = (torch.empty_like(gq), torch.empty_like(gk))
+            self.sets.append((qkv, q, k, gq, gk, out, _lib.strides3(q), _lib.strides3(k)))
+        self.i = 0
+        self.dims = (B, T, H, Hkv, D, R)
+
+    def _next(self):
+        st = self.sets[self.i]
+        self.i = (self.i + 1) % len(self.sets)
+        return st
+
+    def fwd(self):
+        _, q, k, _, _, (oq, ok), sq, sk = self._next()
+        stream = ctypes.c_void_p(self.torch.cuda.current_stream(self.device).cuda_stream)
+        rc = self.lib.hlm_qk_norm_rope_fwd(
+            q.data_ptr(), k.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(), self.table_dtype,
+            oq.data_ptr(), ok.data_ptr(),
+            *self.dims, sq, sk, 1e-6, stream,
+        )
+        assert rc == 0, self.lib.hlm_attn_last_error()
+
+    def bwd(self):
+        _, q, k, gq, gk, (dq, dk), sq, sk = self._next()
+        stream = ctypes.c_void_p(self.torch.cuda.current_stream(self.device).cuda_stream)
+        rc = self.lib.hlm_qk_norm_rope_bwd(
+            q.data_ptr(), k.data_ptr(), gq.data_ptr(), gk.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+            self.table_dtype, dq.data_ptr(), dk.data_ptr(), *self.dims, sq, sk, 1e-6, stream,
+        )
+        assert rc == 0, self.lib.hlm_attn_last_error()
+
+
+def measure_producer(reps: int, warmup: int, device) -> dict:
+    """HIP-event launch times of the producer's forward and backward kernels,
+    against the HBM roofline.  Launches rotate over buffer sets larger than the
+    last-level cache, so each launch's inputs were last touched three launches
+    earlier and come from HBM."""
+    import torch
+
+    cfg = PRODUCER_CONFIG
+    prob = ProducerProblem(cfg, seed=0, device=device)
+    by = producer_bytes(cfg)
+    out = {
+        "op": "q/k RMSNorm + partial RoPE producer (kernels.py:441-658, model.py:101-126)",
+        "workload": f"B={cfg['B']} T={cfg['T']} H=Hkv={cfg['H']} D={cfg['D']} R={cfg['R']}, q/k strided views "
+        f"of a fused projection, bf16, bf16 tables",
+        "bound": "hbm",
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+    }
+    for name, fn in (("fwd", prob.fwd), ("bwd", prob.bwd)):
+        for _ in range(warmup):
+            fn()
+        cold = event_time_ms(torch, fn, reps)
+        achieved = by[name] / (cold * 1e-3) / 1e9
+        kernel = f"qk_norm_rope_kernel<{cfg['D']}, {'true' if name == 'bwd' else 'false'}, bf16 tables>"
+        out[name] = {
+            "kernel": kernel,
+            "launch_us": round(cold * 1e3, 2),
+            "algorithmic_bytes_per_launch": by[name],
+            "achieved": round(achieved, 1),
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": read_traffic("producer_cfg2", f"qk_norm_rope_{name}"),
+        }
+    return out
 
 
 def event_time_ms(torch, fn, reps: int) -> float:
@@ -315,6 +421,7 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time every config (printed to stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step instead of eager launches")
+    ap.add_argument("--no-producer", action="store_true", help="skip the q/k RMSNorm + RoPE producer's timing")
     ap.add_argument(
         "--copy-mib", type=int, default=0,
         help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
@@ -391,6 +498,8 @@ def main() -> int:
         "roofline": r["roofline"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
+    if not args.no_producer:
+        line["producer"] = measure_producer(max(args.steps, 50), 20, device)
     print(json.dumps(line), flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4

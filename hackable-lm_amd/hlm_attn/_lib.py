@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -24,6 +24,9 @@ SIGNATURES = {
 _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P]
 for _name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
     SIGNATURES[_name] = (_I, _BWD_ARGTYPES)
+SIGNATURES["hlm_qk_norm_rope_fwd"] = (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
+SIGNATURES["hlm_qk_norm_rope_bwd"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
+TABLE_F32, TABLE_BF16 = 0, 1  # HLM_TABLE_F32 / HLM_TABLE_BF16
 
 _lib: ctypes.CDLL | None = None
 

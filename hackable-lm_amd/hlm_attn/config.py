@@ -3,6 +3,8 @@
 Mirrors the attention part of hackable-lm's config.py so the hip backend is
 selected and configured exactly like the existing ones:
   ATTENTION_BACKENDS / normalize_attention_backend   config.py:11, :71-77
+  MODULE_BACKENDS / normalize_module_backend         config.py:10, :62-68
+                                                     (qkv_backend picks the q/k producer)
   normalize_attention_window / _full_every           config.py:172-181
   layer_attention_window                             config.py:184-191
 """
@@ -14,6 +16,21 @@ REFERENCE_ATTENTION_BACKENDS = frozenset(
 )
 # The reference's set plus the one backend this library adds.
 ATTENTION_BACKENDS = REFERENCE_ATTENTION_BACKENDS | {HIP_BACKEND}
+
+
+# config.py:10 plus "hip": the fused q/k RMSNorm + RoPE producer of this library.
+REFERENCE_MODULE_BACKENDS = frozenset({"torch", "triton"})
+MODULE_BACKENDS = REFERENCE_MODULE_BACKENDS | {HIP_BACKEND}
+
+
+def normalize_module_backend(name: str, backend: str) -> str:
+    """Lower-cases and validates a module backend such as qkv_backend (config.py:62-68)."""
+    if not isinstance(backend, str):
+        raise ValueError(f"unknown {name} {backend!r}")
+    backend = backend.lower()
+    if backend not in MODULE_BACKENDS:
+        raise ValueError(f"unknown {name} {backend!r}")
+    return backend
 
 
 def normalize_attention_backend(backend: str) -> str:

@@ -73,6 +73,22 @@ struct BwdArgs {
   float scale_log2;  // scale * log2(e)
 };
 
+// Arguments of the fused q/k RMSNorm + partial rotary kernels (qk_norm_rope.hip).
+struct QkNormRopeArgs {
+  const bf16* x[2];   // q, k: (B, T, heads, D), unit D stride
+  const bf16* g[2];   // backward: gradients of the two outputs, contiguous
+  bf16* out[2];       // outputs (forward) or input gradients (backward), contiguous
+  int64_t s[2][3];    // (batch, time, head) strides of q and k in elements
+  int heads[2];       // H, Hkv
+  const void* cos;    // (T, R) rows, fp32 or bf16 (tab_bf16); columns 0 .. R / 2 - 1 are read
+  const void* sin;
+  int tab_bf16;
+  int T, rot;
+  float eps;
+  int rows_q;  // B * T * H
+  int rows;    // B * T * (H + Hkv), < 2^31
+};
+
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }

@@ -13,6 +13,8 @@ template <int D>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases);
+template <int D>
+hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream);
 }  // namespace hlm
 
 namespace {
@@ -70,7 +72,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 2; }
+int hlm_attn_abi_version(void) { return 3; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -177,5 +179,79 @@ extern "C" {
 int hlm_attn_bwd(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdAll, HLM_BWD_ARGS); }
 int hlm_attn_bwd_dq(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDq, HLM_BWD_ARGS); }
 int hlm_attn_bwd_dkdv(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDkDv, HLM_BWD_ARGS); }
+
+}  // extern "C"
+
+namespace {
+
+int run_qk_norm_rope(bool backward, const void* q, const void* k, const void* gq, const void* gk, const void* cos,
+                     const void* sin, int table_dtype, void* oq, void* ok, int B, int T, int H, int Hkv, int D, int rot,
+                     const int64_t* q_strides, const int64_t* k_strides, float eps, void* stream) {
+  g_last_error[0] = '\0';
+  if (B < 0 || T < 0 || H <= 0 || Hkv <= 0)
+    return fail(HLM_ATTN_EINVAL, "bad shape B=%d T=%d H=%d Hkv=%d", B, T, H, Hkv);
+  if (D != 64 && D != 128) return fail(HLM_ATTN_EUNSUPPORTED, "head_dim %d is not supported (64 or 128)", D);
+  if (rot < 0 || rot > D || rot % 16 != 0)
+    return fail(HLM_ATTN_EUNSUPPORTED, "rotary_dim %d must be a multiple of 16 in [0, %d]", rot, D);
+  if (!(eps > 0.f) || !std::isfinite(eps)) return fail(HLM_ATTN_EINVAL, "eps must be positive and finite");
+  if (table_dtype != HLM_TABLE_F32 && table_dtype != HLM_TABLE_BF16)
+    return fail(HLM_ATTN_EINVAL, "table_dtype %d is neither HLM_TABLE_F32 nor HLM_TABLE_BF16", table_dtype);
+  const int64_t rows = (int64_t)B * T * (H + Hkv);
+  if (rows >= ((int64_t)1 << 31) - 1024) return fail(HLM_ATTN_EUNSUPPORTED, "too many rows for one launch");
+  if (rows == 0) return HLM_ATTN_OK;
+  int rc;
+  if ((rc = check_tensor("q", q, q_strides, T, D)) || (rc = check_tensor("k", k, k_strides, T, D))) return rc;
+  const void* outs[2] = {oq, ok};
+  for (int i = 0; i < 2; ++i)
+    if (outs[i] == nullptr || !aligned16(outs[i]))
+      return fail(HLM_ATTN_EINVAL, "output %d is null or not 16-byte aligned", i);
+  if (backward && (gq == nullptr || gk == nullptr || !aligned16(gq) || !aligned16(gk)))
+    return fail(HLM_ATTN_EINVAL, "grad_q_out / grad_k_out are null or not 16-byte aligned");
+  if (rot > 0 && (cos == nullptr || sin == nullptr || !aligned16(cos) || !aligned16(sin)))
+    return fail(HLM_ATTN_EINVAL, "cos / sin are null or not 16-byte aligned");
+  hlm::QkNormRopeArgs a;
+  a.x[0] = static_cast<const hlm::bf16*>(q);
+  a.x[1] = static_cast<const hlm::bf16*>(k);
+  a.g[0] = static_cast<const hlm::bf16*>(gq);
+  a.g[1] = static_cast<const hlm::bf16*>(gk);
+  a.out[0] = static_cast<hlm::bf16*>(oq);
+  a.out[1] = static_cast<hlm::bf16*>(ok);
+  copy3(a.s[0], q_strides);
+  copy3(a.s[1], k_strides);
+  a.heads[0] = H;
+  a.heads[1] = Hkv;
+  a.cos = cos;
+  a.sin = sin;
+  a.tab_bf16 = table_dtype == HLM_TABLE_BF16;
+  a.T = T;
+  a.rot = rot;
+  a.eps = eps;
+  a.rows_q = (int)((int64_t)B * T * H);
+  a.rows = (int)rows;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t err = D == 64 ? hlm::launch_qk_norm_rope<64>(a, backward, s)
+                                 : hlm::launch_qk_norm_rope<128>(a, backward, s);
+  if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "qk_norm_rope launch failed: %s", hipGetErrorString(err));
+  return HLM_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hlm_qk_norm_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, int table_dtype,
+                         void* q_out, void* k_out, int B, int T, int H, int Hkv, int D, int rotary_dim,
+                         const int64_t* q_strides, const int64_t* k_strides, float eps, void* stream) {
+  return run_qk_norm_rope(false, q, k, nullptr, nullptr, cos, sin, table_dtype, q_out, k_out, B, T, H, Hkv, D,
+                          rotary_dim, q_strides, k_strides, eps, stream);
+}
+
+int hlm_qk_norm_rope_bwd(const void* q, const void* k, const void* grad_q_out, const void* grad_k_out,
+                         const void* cos, const void* sin, int table_dtype, void* grad_q, void* grad_k, int B,
+                         int T, int H, int Hkv, int D, int rotary_dim, const int64_t* q_strides,
+                         const int64_t* k_strides, float eps, void* stream) {
+  return run_qk_norm_rope(true, q, k, grad_q_out, grad_k_out, cos, sin, table_dtype, grad_q, grad_k, B, T, H, Hkv,
+                          D, rotary_dim, q_strides, k_strides, eps, stream);
+}
 
 }  // extern "C"

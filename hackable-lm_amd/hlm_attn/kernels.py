@@ -10,6 +10,10 @@ the result is bf16 in (B, T, H, D).  Like the FlashAttention-3/4 branches
 `hip_attention_available` and `resolve_attention_backend` mirror the probe and
 fallback rules of resolve_kernel_backends (kernels.py:146-242) for the
 attention field.
+
+`qk_norm_rope_hip` is the producer step before attention, with the signature
+and semantics of the reference's `qk_norm_rope_triton` (kernels.py:756-771):
+RMSNorm of each q and k row, then the partial rotary embedding.
 """
 from __future__ import annotations
 
@@ -98,3 +102,25 @@ def scaled_dot_product_attention(
     if not is_causal:
         raise RuntimeError(f"{backend} backend implements causal attention only")
     return attention(q, k, v, window_size=window_size)
+
+
+def qk_norm_rope_hip(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused q/k RMSNorm + partial RoPE on the GPU (kernels.py:756-771).
+
+    q (B, T, H, D) and k (B, T, Hkv, D) as QKVProjection._project makes them
+    (model.py:92-99: views of the fused projection, bf16); cos / sin as
+    QKVProjection.fwd_triton passes them (model.py:117-126: the rotary tables
+    transposed to (1, T, 1, R)), or (T, R).  Returns contiguous bf16 q and k.
+    Differentiable.  There is no CPU path: a CPU tensor raises (the reference
+    routes CPU runs to its torch math instead)."""
+    from . import ops
+
+    if q.device.type != "cuda":
+        raise RuntimeError("qk_norm_rope_hip runs on ROCm devices only; use the torch path on the CPU")
+    return ops.hip_qk_norm_rope(q, k, cos, sin, float(eps))

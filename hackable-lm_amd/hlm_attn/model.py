@@ -1,4 +1,5 @@
-"""AttentionCore with the hip backend, mirroring hackable-lm's model.py:129-250.
+"""AttentionCore and QKVProjection with the hip backend, mirroring
+hackable-lm's model.py:129-250 and model.py:50-126.
 
 The reference picks `fwd_<attention_backend>` per call (model.py:169-174);
 this class carries the same per-layer window (model.py:136), the same
@@ -6,6 +7,10 @@ window-or-None rule at call time (model.py:155-159) and the same
 (B, T, H, D) in / (B, T, H, D) out layout as `fwd_flash_attn_2`
 (model.py:216-226).  `fwd_hip` is the method the reference's AttentionCore
 gains when the backend is registered there.
+
+QKVProjection mirrors model.py:76-126: the fused q/k/v projection, then the
+q/k RMSNorm + partial RoPE producer; `fwd_hip` is `fwd_triton` with the HIP
+producer in place of the Triton one, fed the same views and rotary tables.
 
 The reference routes CPU tensors to its own `torch` backend
 (model.py:170); this library has no CPU path and raises instead.
@@ -18,7 +23,12 @@ import torch
 from torch import nn
 
 from . import kernels
-from .config import attention_window_size, layer_attention_window, normalize_attention_backend
+from .config import (
+    attention_window_size,
+    layer_attention_window,
+    normalize_attention_backend,
+    normalize_module_backend,
+)
 
 
 @dataclass
@@ -32,6 +42,78 @@ class AttentionConfig:
     attention_full_every: int | None = 4
     attention_backend: str = "hip"
     dropout: float = 0.0
+    # QKVProjection's fields (config.py:213-232)
+    n_embd: int = 0
+    head_dim: int = 64
+    rope_theta: float = 1_000_000.0
+    rope_fraction: float = 0.25
+    norm_eps: float = 1e-6
+    qkv_backend: str = "hip"
+
+
+class RotaryEmbedding(nn.Module):
+    """model.py:50-70: cos / sin tables (1, 1, T, R) over R = int(dim * fraction)
+    rounded down to even, both halves repeating the R / 2 frequencies
+    theta^(-2j/R); cached for the longest sequence seen, returned in `dtype`."""
+
+    def __init__(self, dim: int, theta: float = 1_000_000.0, fraction: float = 0.25) -> None:
+        super().__init__()
+        rotary_dim = int(dim * fraction)
+        self.rotary_dim = rotary_dim - rotary_dim % 2
+        exponents = torch.arange(0, self.rotary_dim, 2).float() / self.rotary_dim
+        self.register_buffer("inv_freq", 1.0 / (theta ** exponents), persistent=False)
+        self._cached_len = 0
+        self._cos: torch.Tensor | None = None
+        self._sin: torch.Tensor | None = None
+
+    def forward(self, seq_len: int, device: torch.device, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._cos is None or seq_len > self._cached_len or self._cos.device != device:
+            positions = torch.arange(seq_len, device=device, dtype=torch.float32)
+            angles = torch.outer(positions, self.inv_freq.to(device))
+            angles = torch.cat((angles, angles), dim=-1)
+            self._cos, self._sin = angles.cos()[None, None], angles.sin()[None, None]
+            self._cached_len = seq_len
+        return self._cos[:, :, :seq_len].to(dtype=dtype), self._sin[:, :, :seq_len].to(dtype=dtype)
+
+
+class QKVProjection(nn.Module):
+    """model.py:76-126 with the hip producer.  The projection's q and k are
+    views of one (B, T, (H + 2 Hkv) D) tensor; the producer reads them in
+    place through their strides and writes contiguous normalised, rotated
+    q and k; v stays the view."""
+
+    def __init__(self, config: AttentionConfig, layer_idx: int) -> None:
+        super().__init__()
+        del layer_idx
+        self.config = config
+        self.n_head = config.n_head
+        self.n_kv_head = config.n_kv_head
+        self.head_dim = config.head_dim
+        self.q_dim = config.n_head * config.head_dim
+        self.kv_dim = config.n_kv_head * config.head_dim
+        self.qkv_proj = nn.Linear(config.n_embd, self.q_dim + 2 * self.kv_dim, bias=False)
+        self.rope = RotaryEmbedding(config.head_dim, config.rope_theta, config.rope_fraction)
+
+    def _project(self, x: torch.Tensor):
+        bsz, seq_len, _ = x.shape
+        q, k, v = self.qkv_proj(x).split((self.q_dim, self.kv_dim, self.kv_dim), dim=-1)
+        q = q.view(bsz, seq_len, self.n_head, self.head_dim)
+        k = k.view(bsz, seq_len, self.n_kv_head, self.head_dim)
+        v = v.view(bsz, seq_len, self.n_kv_head, self.head_dim)
+        cos, sin = self.rope(seq_len, x.device, q.dtype)
+        return q, k, v, cos, sin
+
+    def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        backend = normalize_module_backend("qkv_backend", self.config.qkv_backend)
+        fwd_backend = getattr(self, f"fwd_{backend}", None)
+        if fwd_backend is None:
+            raise RuntimeError(f"{type(self).__name__} does not support backend {backend!r}")
+        return fwd_backend(x)
+
+    def fwd_hip(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        q, k, v, cos, sin = self._project(x)
+        q, k = kernels.qk_norm_rope_hip(q, k, cos.transpose(1, 2), sin.transpose(1, 2), self.config.norm_eps)
+        return q, k, v
 
 
 class AttentionCore(nn.Module):

@@ -147,3 +147,125 @@ def _backward(ctx, dout, _dlse):
 
 
 hip_attn_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+# --- the producer step: fused q/k RMSNorm + partial rotary embedding ---------------
+#
+# hackable_lm::hip_qk_norm_rope mirrors the reference's Triton op
+# hackable_lm::qk_norm_rope (/root/reference/kernels.py:505-535, autograd
+# :679-741): same inputs (q, k, cos, sin, eps), outputs contiguous in q's and
+# k's shapes, backward through the fused kernel.
+
+
+def _rope_table(t: torch.Tensor, T: int) -> tuple[torch.Tensor, int]:
+    """cos / sin in any of the reference's broadcast shapes ((T, R),
+    (1, T, 1, R) after its transpose, (1, 1, T, R)) as a contiguous (T, R)
+    table and its HLM_TABLE_* code: bf16 tables (the model's, model.py:62-70)
+    and fp32 tables are read as they are, other types are converted to fp32."""
+    R = t.shape[-1]
+    if t.numel() != T * R:
+        raise RuntimeError(f"rotary table of shape {tuple(t.shape)} does not hold {T} rows of {R}")
+    if t.dtype not in (_BF16, torch.float32):
+        t = t.to(torch.float32)
+    code = _lib.TABLE_BF16 if t.dtype == _BF16 else _lib.TABLE_F32
+    t = t.reshape(T, R).contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t, code
+
+
+def _check_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor) -> None:
+    if q.device.type != "cuda":
+        raise RuntimeError(f"hip qk_norm_rope runs on ROCm devices only, got a tensor on {q.device}")
+    for name, t in (("q", q), ("k", k)):
+        if t.dtype != _BF16:
+            raise RuntimeError(f"hip qk_norm_rope expects bfloat16 {name}, got {t.dtype}")
+        if t.dim() != 4:
+            raise RuntimeError(f"hip qk_norm_rope expects {name} shaped (B, T, heads, D), got {tuple(t.shape)}")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise RuntimeError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree on B, T or D")
+    if k.device != q.device or cos.device != q.device:
+        raise RuntimeError("q, k, cos and sin must be on the same device")
+
+
+@torch.library.custom_op("hackable_lm::hip_qk_norm_rope", mutates_args=())
+def hip_qk_norm_rope(
+    q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    _check_qk(q, k, cos)
+    lib = _lib.load()
+    q, k = _kernel_ready(q), _kernel_ready(k)
+    B, T, H, D = q.shape
+    Hkv = k.shape[2]
+    c, code = _rope_table(cos, T)
+    s, _ = _rope_table(sin.to(c.dtype), T)
+    q_out = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
+    k_out = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.hlm_qk_norm_rope_fwd(
+            q.data_ptr(), k.data_ptr(), c.data_ptr(), s.data_ptr(), code, q_out.data_ptr(), k_out.data_ptr(),
+            B, T, H, Hkv, D, c.shape[1], _lib.strides3(q), _lib.strides3(k), float(eps),
+            _stream_handle(q.device),
+        )
+    _lib.check(rc, lib)
+    return q_out, k_out
+
+
+@hip_qk_norm_rope.register_fake
+def _(q, k, cos, sin, eps):
+    return q.new_empty(q.shape, dtype=_BF16), k.new_empty(k.shape, dtype=_BF16)
+
+
+@torch.library.custom_op("hackable_lm::hip_qk_norm_rope_backward", mutates_args=())
+def hip_qk_norm_rope_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    grad_q: torch.Tensor,
+    grad_k: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    _check_qk(q, k, cos)
+    lib = _lib.load()
+    q, k = _kernel_ready(q), _kernel_ready(k)
+    B, T, H, D = q.shape
+    Hkv = k.shape[2]
+    gq = grad_q.to(_BF16).contiguous()
+    gk = grad_k.to(_BF16).contiguous()
+    c, code = _rope_table(cos, T)
+    s, _ = _rope_table(sin.to(c.dtype), T)
+    dq = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
+    dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.hlm_qk_norm_rope_bwd(
+            q.data_ptr(), k.data_ptr(), gq.data_ptr(), gk.data_ptr(), c.data_ptr(), s.data_ptr(), code,
+            dq.data_ptr(), dk.data_ptr(), B, T, H, Hkv, D, c.shape[1],
+            _lib.strides3(q), _lib.strides3(k), float(eps), _stream_handle(q.device),
+        )
+    _lib.check(rc, lib)
+    return dq, dk
+
+
+@hip_qk_norm_rope_backward.register_fake
+def _(q, k, grad_q, grad_k, cos, sin, eps):
+    return q.new_empty(q.shape, dtype=_BF16), k.new_empty(k.shape, dtype=_BF16)
+
+
+def _qk_setup_context(ctx, inputs, output):
+    q, k, cos, sin, eps = inputs
+    ctx.save_for_backward(q, k, cos, sin)
+    ctx.eps = eps
+
+
+def _qk_backward(ctx, grad_q, grad_k):
+    q, k, cos, sin = ctx.saved_tensors
+    if grad_q is None:
+        grad_q = torch.zeros_like(q, memory_format=torch.contiguous_format)
+    if grad_k is None:
+        grad_k = torch.zeros_like(k, memory_format=torch.contiguous_format)
+    dq, dk = hip_qk_norm_rope_backward(q, k, grad_q, grad_k, cos, sin, ctx.eps)
+    return dq, dk, None, None, None
+
+
+hip_qk_norm_rope.register_autograd(_qk_backward, setup_context=_qk_setup_context)

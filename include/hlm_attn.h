@@ -48,6 +48,10 @@ extern "C" {
 #define HLM_ATTN_EUNSUPPORTED (-2) /* valid request this library does not implement */
 #define HLM_ATTN_ELAUNCH (-3)     /* the HIP runtime rejected a kernel launch */
 
+/* Element types of the rotary tables (cos, sin) of hlm_qk_norm_rope_*. */
+#define HLM_TABLE_F32 0
+#define HLM_TABLE_BF16 1
+
 /* ABI revision of this header; bumped on any signature change. */
 int hlm_attn_abi_version(void);
 
@@ -103,6 +107,42 @@ int hlm_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* o
                       const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
                       const int64_t* dk_strides, const int64_t* dv_strides,
                       int window, float scale, void* stream);
+
+/*
+ * The producer step before attention: fused RMSNorm (no weight) and partial
+ * rotary embedding of q and k, forward and backward.  Per (batch, time, head)
+ * row x of D values, in fp32:
+ *   z = x * rsqrt(mean(x^2) + eps),
+ *   out[d] = z[d] c - z[d+h] s (d < h), z[d] c + z[d-h] s (h <= d < R), z[d] (d >= R),
+ * with R = rotary_dim, h = R / 2, c = cos[t * R + d mod h], s = sin[...].
+ * q (B, T, H, D) and k (B, T, Hkv, D) are bf16 with unit D stride and
+ * {stride_b, stride_t, stride_h} element strides (multiples of 8, 16-byte
+ * aligned bases; stride_t >= D); cos and sin are (T, R) contiguous, 16-byte
+ * aligned, of element type table_dtype (HLM_TABLE_F32 or HLM_TABLE_BF16: the
+ * model's tables are bf16, model.py:62-70, and are read as they are);
+ * q_out / k_out are bf16 and contiguous.  D in {64, 128}; R a multiple of 16
+ * with 0 <= R <= D; B * T * (H + Hkv) < 2^31 - 1024; eps > 0.
+ * Replaces kernels.qk_norm_rope_triton / the hackable_lm::qk_norm_rope Triton
+ * op (/root/reference/kernels.py:441-535, :756-771), the math of
+ * QKVProjection.fwd_torch (/root/reference/model.py:101-115).
+ */
+int hlm_qk_norm_rope_fwd(const void* q, const void* k, const void* cos, const void* sin, int table_dtype,
+                         void* q_out, void* k_out, int B, int T, int H, int Hkv, int D, int rotary_dim,
+                         const int64_t* q_strides, const int64_t* k_strides, float eps, void* stream);
+
+/*
+ * Its backward: given q, k (the forward's inputs) and grad_q_out, grad_k_out
+ * (bf16, contiguous, the gradients of q_out / k_out), writes grad_q, grad_k
+ * (bf16, contiguous):  gn = the rotation transposed applied to grad_out,
+ * grad_x = r (gn - z mean(gn z)), r = rsqrt(mean(x^2) + eps).
+ * Replaces the hackable_lm::qk_norm_rope_backward Triton op
+ * (/root/reference/kernels.py:541-665) and its CPU closed form
+ * (/root/reference/kernels.py:703-741).
+ */
+int hlm_qk_norm_rope_bwd(const void* q, const void* k, const void* grad_q_out, const void* grad_k_out,
+                         const void* cos, const void* sin, int table_dtype, void* grad_q, void* grad_k,
+                         int B, int T, int H, int Hkv, int D, int rotary_dim,
+                         const int64_t* q_strides, const int64_t* k_strides, float eps, void* stream);
 
 /* Message describing the last failed call on this thread ("" if none). */
 const char* hlm_attn_last_error(void);

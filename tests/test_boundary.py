@@ -26,7 +26,7 @@ HEADER = REPO / "include" / "hlm_attn.h"
 
 def declared_symbols() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(hlm_attn_\w+)\s*\(", text))
+    return set(re.findall(r"\b(hlm_(?:attn|qk)_\w+)\s*\(", text))
 
 
 # --- the shared library -------------------------------------------------------
@@ -258,3 +258,116 @@ def test_flop_model_matches_bench():
     assert round(f["fwd"] / 1e9, 3) == 22.555 and round(f["bwd"] / 1e9, 3) == 45.110
     assert f["bwd_dq"] + f["bwd_dkdv"] == f["bwd"]
     assert math.isclose(bench.PEAK_BF16_TFLOPS, 256 * 4096 * 2.4e9 / 1e12, rel_tol=1e-4)
+
+
+# --- q/k RMSNorm + partial RoPE producer --------------------------------------------
+
+def _qk(lib, backward=False, ptr=0x1000, B=1, T=16, H=2, Hkv=2, D=64, rot=16, strides=(2048, 128, 64), eps=1e-6,
+        table=0x3000, table_dtype=_lib.TABLE_BF16):
+    s = _strides(*strides)
+    p = ctypes.c_void_p(ptr) if ptr else None
+    t = ctypes.c_void_p(table) if table else None
+    out = ctypes.c_void_p(0x2000)
+    if backward:
+        return lib.hlm_qk_norm_rope_bwd(p, p, out, out, t, t, table_dtype, out, out, B, T, H, Hkv, D, rot, s, s, eps,
+                                        None)
+    return lib.hlm_qk_norm_rope_fwd(p, p, t, t, table_dtype, out, out, B, T, H, Hkv, D, rot, s, s, eps, None)
+
+
+@pytest.mark.parametrize("backward", [False, True])
+@pytest.mark.parametrize(
+    "kwargs,code,msg",
+    [
+        (dict(D=32), -2, "head_dim 32"),
+        (dict(rot=8), -2, "rotary_dim 8"),
+        (dict(rot=80), -2, "rotary_dim 80"),
+        (dict(rot=-16), -2, "rotary_dim -16"),
+        (dict(H=0), -1, "bad shape"),
+        (dict(eps=0.0), -1, "eps"),
+        (dict(eps=float("inf")), -1, "eps"),
+        (dict(ptr=None), -1, "null pointer"),
+        (dict(ptr=0x1008), -1, "16-byte aligned"),
+        (dict(strides=(2048, 100, 64)), -1, "multiple of 8"),
+        (dict(table=None), -1, "cos / sin"),
+        (dict(table=0x3004), -1, "cos / sin"),
+        (dict(table_dtype=2), -1, "table_dtype 2"),
+    ],
+)
+def test_qk_norm_rope_rejects_bad_arguments_before_touching_the_device(backward, kwargs, code, msg):
+    lib = _lib.load()
+    assert _qk(lib, backward, **kwargs) == code
+    assert msg in lib.hlm_attn_last_error().decode()
+
+
+def test_qk_norm_rope_empty_problems_are_no_ops():
+    lib = _lib.load()
+    for backward in (False, True):
+        assert _qk(lib, backward, B=0) == 0
+        assert _qk(lib, backward, T=0) == 0
+        assert lib.hlm_attn_last_error() == b""
+    # R = 0 needs no tables (plain RMSNorm): validation passes without them
+    assert _qk(lib, B=0, rot=0, table=None) == 0
+
+
+def test_qk_norm_rope_refuses_cpu_tensors_and_describes_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    q = torch.randn(1, 8, 2, 64).bfloat16()
+    cos = torch.zeros(8, 16)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        hlm_attn.qk_norm_rope_hip(q, q, cos, cos, 1e-6)
+    with FakeTensorMode():
+        q = torch.empty(2, 40, 8, 64, dtype=torch.bfloat16)
+        k = torch.empty(2, 40, 2, 64, dtype=torch.bfloat16)
+        c = torch.empty(1, 40, 1, 16)
+        qo_, ko_ = ops.hip_qk_norm_rope(q, k, c, c, 1e-6)
+        assert qo_.shape == q.shape and ko_.shape == k.shape and qo_.dtype == torch.bfloat16
+        dq, dk = ops.hip_qk_norm_rope_backward(q, k, q, k, c, c, 1e-6)
+        assert dq.shape == q.shape and dk.shape == k.shape
+
+
+def test_rope_table_accepts_the_reference_layouts():
+    t = torch.arange(12.0).reshape(3, 4)
+    for view in (t, t[None, :, None, :], t[None, None], t[None, None].transpose(1, 2)):
+        got, code = ops._rope_table(view, 3)
+        assert got.shape == (3, 4) and got.is_contiguous() and torch.equal(got, t) and code == _lib.TABLE_F32
+    # bf16 tables (the model's) are passed as they are; other types become fp32
+    got, code = ops._rope_table(t.bfloat16()[None, None], 3)
+    assert got.dtype == torch.bfloat16 and code == _lib.TABLE_BF16
+    got, code = ops._rope_table(t.half(), 3)
+    assert got.dtype == torch.float32 and code == _lib.TABLE_F32
+    # a prefix of a longer cached table (RotaryEmbedding slices its cache)
+    cache = torch.arange(40.0).reshape(1, 1, 10, 4)
+    got, _ = ops._rope_table(cache[:, :, :3].transpose(1, 2), 3)
+    assert torch.equal(got, cache[0, 0, :3])
+    with pytest.raises(RuntimeError, match="does not hold"):
+        ops._rope_table(t, 4)
+
+
+def test_rotary_embedding_matches_the_oracle_tables():
+    from oracle import qk_norm_rope as qo
+
+    for dim, fraction in ((64, 0.25), (128, 0.25), (64, 1.0), (10, 0.25)):
+        rope = model.RotaryEmbedding(dim, fraction=fraction)
+        cos, sin = rope(33, torch.device("cpu"), torch.float32)
+        rc, rs = qo.rotary_tables(33, dim, fraction=fraction)
+        assert cos.shape == (1, 1, 33, rope.rotary_dim)
+        assert torch.equal(cos[0, 0], rc) and torch.equal(sin[0, 0], rs)
+    # cached for the longest length seen; shorter calls slice it
+    c5, _ = rope(5, torch.device("cpu"), torch.bfloat16)
+    assert c5.dtype == torch.bfloat16 and torch.equal(c5[0, 0], qo.rotary_tables(5, 10)[0].bfloat16())
+
+
+def test_qkv_projection_dispatches_on_qkv_backend():
+    cfg = model.AttentionConfig(n_layer=1, n_head=2, n_kv_head=1, n_embd=32, head_dim=64)
+    proj = model.QKVProjection(cfg, 0)
+    assert proj.qkv_proj.weight.shape == ((2 + 2) * 64, 32)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        proj.to(torch.bfloat16)(torch.randn(1, 4, 32).bfloat16())
+    for backend, exc, match in (("triton", RuntimeError, "does not support backend"),
+                                ("cuda", ValueError, "unknown qkv_backend")):
+        cfg_b = model.AttentionConfig(n_layer=1, n_head=2, n_kv_head=1, n_embd=32, head_dim=64, qkv_backend=backend)
+        with pytest.raises(exc, match=match):
+            model.QKVProjection(cfg_b, 0)(torch.randn(1, 4, 32))
+    assert config.MODULE_BACKENDS == {"torch", "triton", "hip"}
+    assert config.normalize_module_backend("qkv_backend", "HIP") == "hip"
