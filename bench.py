@@ -14,7 +14,9 @@ MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
 (HIP-event timed on the launch stream) and the CPU baseline: the reference's
 `torch` backend restated on the host CPU (configs[0] shape, fp32, forward).
 A "producer" object times the q/k RMSNorm + partial RoPE kernels that feed
-attention (forward and backward) at cfg2's q/k shape against the HBM roofline.
+attention (forward and backward) at cfg2's q/k shape against the HBM roofline;
+an "eval" object times the evaluation harness's no-grad forwards at batch 1
+and ragged T.
 
 Steps are eager launches by default (they run ahead of the GPU); --graph times
 HIP-graph replays of one captured step instead (the way a training step runs
@@ -22,7 +24,7 @@ under torch.compile's CUDA-graph mode).  The default warmup (300 steps) lets
 the GPU reach its steady clock before timing starts.
 
   python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline] [--graph]
-                  [--no-producer]
+                  [--no-producer] [--no-eval]
 """
 from __future__ import annotations
 
@@ -243,6 +245,47 @@ def measure_producer(reps: int, warmup: int, device) -> dict:
     return out
 
 
+EVAL_SHAPES = ((1, 128), (1, 512), (1, 1024), (1, 2048), (8, 2048))  # (B, T) at H=12, D=64
+
+
+def measure_eval(reps: int, device) -> dict:
+    """The evaluation harness's calls (lm_eval_hackable_lm.py:134-160,185-207):
+    no-grad forwards at batch 1 and ragged T, without a KV cache, through
+    hlm_attn.attention (which skips the op dispatcher when nothing needs
+    autograd).  Per shape and window: `call_us`, HIP-event time per call over
+    back-to-back calls (host and GPU overlapped, what an evaluation loop
+    sees); `kernel_us`, the same through the C ABI alone (GPU-bound); the
+    split count the library chose."""
+    import torch
+
+    import hlm_attn
+
+    lib = None
+    out = {"workload": "no-grad forwards, H=12 D=64, windows 512 and causal; synthetic N(0,1) bf16", "shapes": []}
+    for B, T in EVAL_SHAPES:
+        for W in (512, None):
+            cfg = dict(B=B, T=T, H=12, D=64, W=W)
+            prob = Problem(cfg, seed=0, device=device)
+            lib = prob.lib
+            call = lambda: hlm_attn.attention(prob.q, prob.k, prob.v, window_size=W)  # noqa: E731
+            with torch.no_grad():
+                for _ in range(20):
+                    call()
+                call_ms = event_time_ms(torch, call, reps)
+            for _ in range(20):
+                prob.fwd()
+            kern_ms = event_time_ms(torch, prob.fwd, reps)
+            fl = 4 * cfg["D"] * pairs(T, W) * B * cfg["H"]
+            out["shapes"].append({
+                "B": B, "T": T, "window": W,
+                "nsplit": lib.hlm_attn_fwd_split_count(B, T, 12, 64, 0 if W is None else W),
+                "call_us": round(call_ms * 1e3, 2),
+                "kernel_us": round(kern_ms * 1e3, 2),
+                "tflops": round(fl / (call_ms * 1e-3) / 1e12, 1),
+            })
+    return out
+
+
 def event_time_ms(torch, fn, reps: int) -> float:
     """Average duration of fn's launches, by HIP events on the launch stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -422,6 +465,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step instead of eager launches")
     ap.add_argument("--no-producer", action="store_true", help="skip the q/k RMSNorm + RoPE producer's timing")
+    ap.add_argument("--no-eval", action="store_true", help="skip the evaluation-path (no-grad, batch 1) timings")
     ap.add_argument(
         "--copy-mib", type=int, default=0,
         help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
@@ -500,6 +544,8 @@ def main() -> int:
     }
     if not args.no_producer:
         line["producer"] = measure_producer(max(args.steps, 50), 20, device)
+    if not args.no_eval:
+        line["eval"] = measure_eval(max(args.steps // 2, 50), device)
     print(json.dumps(line), flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -24,6 +24,8 @@ SIGNATURES = {
 _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P]
 for _name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
     SIGNATURES[_name] = (_I, _BWD_ARGTYPES)
+SIGNATURES["hlm_attn_fwd_split"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _S, _S, _I, _F, _P])
+SIGNATURES["hlm_attn_fwd_split_count"] = (_I, [_I, _I, _I, _I, _I])
 SIGNATURES["hlm_qk_norm_rope_fwd"] = (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
 SIGNATURES["hlm_qk_norm_rope_bwd"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
 TABLE_F32, TABLE_BF16 = 0, 1  # HLM_TABLE_F32 / HLM_TABLE_BF16
@@ -60,10 +62,20 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     return lib
 
 
+_Strides = ctypes.c_int64 * 3
+_strides_cache: dict = {}
+
+
 def strides3(t) -> ctypes.Array:
-    """(batch, time, head) strides of a (B, T, H, D) tensor as an int64[3]."""
-    s = t.stride()
-    return (ctypes.c_int64 * 3)(s[0], s[1], s[2])
+    """(batch, time, head) strides of a (B, T, H, D) tensor as an int64[3]
+    (shared per distinct stride triple; the library only reads it)."""
+    s = t.stride()[:3]
+    arr = _strides_cache.get(s)
+    if arr is None:
+        if len(_strides_cache) > 4096:
+            _strides_cache.clear()
+        arr = _strides_cache[s] = _Strides(*s)
+    return arr
 
 
 def check(rc: int, lib: ctypes.CDLL) -> None:

@@ -54,6 +54,13 @@ struct FwdArgs {
   int64_t sq[3], sk[3], sv[3], so[3];  // (batch, time, head) strides in elements
   int B, T, H, Hkv, W;                 // 1 <= W <= T
   float scale_log2;                    // softmax scale * log2(e)
+  // Split-key forward only: nsplit workgroups share one query tile's key
+  // range; each writes its unnormalised O rows (fp32, part_o[s][b*H+h][t][D])
+  // and per-row (running max in log2 units, row sum) pairs
+  // (part_ml[s][b*H+h][t][2]) for the combine kernel.
+  float* part_o;
+  float* part_ml;
+  int nsplit;
 };
 
 struct BwdArgs {

@@ -36,7 +36,7 @@ namespace hlm {
 
 constexpr float kSumLimit = 0x1p64f;  // a tile's row sum above this (or NaN) forces the exact path
 
-template <int D, int NBUF, int PRE>
+template <int D, int NBUF, int PRE, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   using L = CS<D>;
   constexpr int NW = 4, BM = NW * 32, BN = 64;
@@ -54,8 +54,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
 
   const int T = a.T, W = a.W, H = a.H;
   const int nqt = (T + BM - 1) / BM;
+  // Split-key launches repeat the grid of tiles nsplit times, split index
+  // outermost (so the XCD grouping of tile_order holds within each repeat).
+  int bid = blockIdx.x, split = 0;
+  if constexpr (SPLIT) {
+    const int units = nqt * a.B * H;
+    split = bid / units;
+    bid -= split * units;
+  }
   // Query tiles with q0 >= W - 1 see a full window: they are ranks 0 .. n_full - 1.
-  const TileId tid_ = tile_order(blockIdx.x, a.B * H, nqt - (W - 1 + BM - 1) / BM);
+  const TileId tid_ = tile_order(bid, a.B * H, nqt - (W - 1 + BM - 1) / BM);
   const int qt = nqt - 1 - tid_.rank;  // longest causal rows first
   const int bh = tid_.unit;
   const int h = bh % H, b = bh / H;
@@ -73,15 +81,32 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   const unsigned lring = lds_addr(ring);
   const unsigned stg_q = lring + PRE * SLOTB + wave * WSTG;
 
+  // The key tiles this workgroup visits: all that meet [q0 - W + 1, q_last],
+  // or with split-key launches the split-th of nsplit equal runs of them.
+  const int key_lo = max(0, q0 - W + 1);
+  const int key_hi = min(T, q0 + BM) - 1;
+  int t_lo = key_lo / BN, n_tiles = key_hi / BN - t_lo + 1;
+  if constexpr (SPLIT) {
+    const int per = (n_tiles + a.nsplit - 1) / a.nsplit;
+    t_lo += split * per;
+    n_tiles = min(per, n_tiles - split * per);
+    if (n_tiles <= 0) {  // nothing to visit: rows marked empty (sum 0) for the combine
+      const int myq = qw0 + l32;
+      if (myq < T && h32 == 0) {
+        const int64_t prow = ((int64_t)split * a.B * H + bh) * T + myq;
+        a.part_ml[2 * prow] = -INFINITY;
+        a.part_ml[2 * prow + 1] = 0.f;
+      }
+      return;
+    }
+  }
+
   // 1. This wave's Q rows into the staging area (cs layout).
 #pragma unroll
   for (int k = 0; k < NCH; ++k)
     lds_dma_at<16>(rq, stg_q + k * 1024, (qw0 + L::dma_row(k, lane)) * sq2 + L::dma_col_bytes(k, lane));
 
   // 2. The first key tiles.
-  const int key_lo = max(0, q0 - W + 1);
-  const int key_hi = min(T, q0 + BM) - 1;
-  const int t_lo = key_lo / BN, n_tiles = key_hi / BN - t_lo + 1;
   int kof[CPT / NW], vof[CPT / NW];
 #pragma unroll
   for (int i = 0; i < CPT / NW; ++i) {
@@ -207,6 +232,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
         oacc[db] = mfma32(cs_operand_tr<D>(vt, tro[db][0], tro[db][1], 16 * kk), pb[kk], oacc[db]);
   }
 
+  if constexpr (SPLIT) {
+    // Unnormalised O (fp32) and the row's (max, sum): lane (l32, h32) holds
+    // O[qw0 + l32][32 db + 8 i + 4 h32 + j] in oacc[db][4 i + j].  Every
+    // issued tile has been waited for inside the loop, so no copy into LDS is
+    // still in flight when the wave ends.
+    const float ltot = lsum + __shfl_xor(lsum, 32);
+    const int myq = qw0 + l32;
+    if (myq < T) {
+      const int64_t prow = ((int64_t)split * a.B * H + bh) * T + myq;
+      float* po = a.part_o + prow * D + 4 * h32;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v4[j] = oacc[db][4 * i + j];
+          *reinterpret_cast<f32x4*>(po + 32 * db + 8 * i) = v4;
+        }
+      if (h32 == 0) {
+        a.part_ml[2 * prow] = m;
+        a.part_ml[2 * prow + 1] = ltot;
+      }
+    }
+    return;
+  }
+
   // O through LDS (whole rows leave with coalesced stores); lse from lanes 0..31.
   dma_barrier<0>();
   int ln = lane;
@@ -235,6 +287,49 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   if (myq < T && h32 == 0) a.lse[(int64_t)bh * T + myq] = (m + __log2f(ltot)) * kLn2;
 }
 
+// Merges the nsplit partial results of a split-key forward: per query row,
+// M = max_s m_s, L = sum_s l_s 2^(m_s - M), O = sum_s O_s 2^(m_s - M) / L and
+// lse = (M + log2 L) ln 2.  Splits that saw no visible key (l_s = 0) are
+// skipped (their O rows were never written).  One thread per 8 values of a
+// row; every row has at least one visible key (itself), so L > 0.
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdArgs a) {
+  constexpr int LPR = D / 8;
+  const int64_t rows = (int64_t)a.B * a.H * a.T;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / LPR;
+  const int c = (int)(gid % LPR);
+  if (row >= rows) return;
+  const int64_t split_stride = rows;  // rows per split
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[2 * (s * split_stride + row)]);
+  float L = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const int64_t prow = s * split_stride + row;
+    const float l = a.part_ml[2 * prow + 1];
+    if (!(l > 0.f)) continue;
+    const float w = exp2f(a.part_ml[2 * prow] - M);
+    L = fmaf(l, w, L);
+    const float* po = a.part_o + prow * D + 8 * c;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(po), hi = *reinterpret_cast<const f32x4*>(po + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] = fmaf(lo[e], w, acc[e]);
+      acc[e + 4] = fmaf(hi[e], w, acc[e + 4]);
+    }
+  }
+  const float inv = 1.f / L;
+  const int t = (int)(row % a.T);
+  const int bh = (int)(row / a.T), h = bh % a.H, b = bh / a.H;
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (bf16)(acc[e] * inv);
+  *reinterpret_cast<bf16x8*>(a.o + b * a.so[0] + t * a.so[1] + h * a.so[2] + 8 * c) = o;
+  if (c == 0) a.lse[row] = (M + __log2f(L)) * kLn2;
+}
+
 template <int D>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   constexpr int BM = 128;
@@ -243,12 +338,49 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
   // D = 64: three slots of 16 KB (three workgroups per CU), the Q staging in
   // the third behind two tiles in flight; D = 128: two slots of 32 KB (two
   // per CU), the staging in the second behind one tile in flight.
+  if (a.nsplit <= 1) {
+    if constexpr (D == 64)
+      hipLaunchKernelGGL((attn_fwd_kernel<D, 3, 2, false>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<D, 2, 1, false>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    return hipGetLastError();
+  }
+  const unsigned sblocks = (unsigned)(blocks * a.nsplit);
   if constexpr (D == 64)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, 3, 2>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, 3, 2, true>), dim3(sblocks), dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, 2, 1>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, 2, 1, true>), dim3(sblocks), dim3(kThreads), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int64_t threads = (int64_t)a.B * a.H * a.T * (D / 8);
+  hipLaunchKernelGGL((attn_fwd_combine_kernel<D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
+
+// Splits for a small forward grid.  A workgroup alone on a CU runs a key
+// tile in about 1 us (latency-bound), three sharing a CU about 2.1 us each,
+// and the merge pass costs 4-10 us (measured on the MI355X at B = 1, H = 12,
+// D = 64).  So splitting pays only when the longest row is long: 1 (no
+// split) when the tiles already occupy half of the workgroup slots or the
+// longest row has fewer than 24 key tiles; otherwise one split per 12 key
+// tiles of the longest row, at most enough to fill the slots and at most
+// kMaxSplit.  (B = 1, T = 2048, causal: 33.7 us unsplit, 28 us in 2 splits;
+// with a 512-key window, or at T = 1024, splitting is slower.)
+template <int D>
+int fwd_split_count(int B, int T, int H, int W) {
+  constexpr int BM = 128, BN = 64, kMaxSplit = 16, kMinTiles = 24, kTilesPerSplit = 12;
+  const int slots = 256 * (D == 64 ? 3 : 2);  // resident workgroups on the MI355X
+  const int64_t units = (int64_t)((T + BM - 1) / BM) * B * H;
+  if (units == 0 || 2 * units >= slots) return 1;
+  const int longest = (min(T, W + BM - 1) + BN - 1) / BN + 1;  // key tiles of the longest row
+  if (longest < kMinTiles) return 1;
+  const int fill = (int)((slots + units - 1) / units);
+  const int n = min(min(longest / kTilesPerSplit, fill), kMaxSplit);
+  return n >= 2 ? n : 1;
+}
+
+template int fwd_split_count<64>(int, int, int, int);
+template int fwd_split_count<128>(int, int, int, int);
 
 template hipError_t launch_fwd<64>(const FwdArgs&, hipStream_t);
 template hipError_t launch_fwd<128>(const FwdArgs&, hipStream_t);

@@ -12,6 +12,8 @@ namespace hlm {
 template <int D>
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 template <int D>
+int fwd_split_count(int B, int T, int H, int W);
+template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases);
 template <int D>
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream);
@@ -72,17 +74,26 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 3; }
+int hlm_attn_abi_version(void) { return 4; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
-int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int T, int H,
-                 int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
-                 const int64_t* v_strides, const int64_t* o_strides, int window, float scale,
-                 void* stream) {
+}  // extern "C"
+
+namespace {
+
+int run_fwd(const void* q, const void* k, const void* v, void* o, float* lse, float* ws, int nsplit, int B, int T,
+            int H, int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, int window, float scale, void* stream) {
   g_last_error[0] = '\0';
   int rc = check_dims(B, T, H, Hkv, D, scale);
   if (rc) return rc;
+  if (nsplit < 1 || nsplit > HLM_ATTN_MAX_SPLIT)
+    return fail(HLM_ATTN_EINVAL, "nsplit %d is outside [1, %d]", nsplit, HLM_ATTN_MAX_SPLIT);
+  if (nsplit > 1 && (ws == nullptr || !aligned16(ws)))
+    return fail(HLM_ATTN_EINVAL, "split workspace is null or not 16-byte aligned");
+  if (nsplit > 1 && (int64_t)B * H * T * (D / 8) >= ((int64_t)1 << 38))
+    return fail(HLM_ATTN_EUNSUPPORTED, "problem too large for a split-key forward");
   if (B == 0 || T == 0) return HLM_ATTN_OK;
   if ((rc = check_tensor("q", q, q_strides, T, D)) || (rc = check_tensor("k", k, k_strides, T, D)) ||
       (rc = check_tensor("v", v, v_strides, T, D)) || (rc = check_tensor("o", o, o_strides, T, D)))
@@ -104,10 +115,39 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   a.Hkv = Hkv;
   a.W = effective_window(window, T);
   a.scale_log2 = scale * hlm::kLog2e;
+  a.nsplit = nsplit;
+  a.part_o = ws;
+  a.part_ml = ws == nullptr ? nullptr : ws + (int64_t)nsplit * B * H * T * D;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t err = D == 64 ? hlm::launch_fwd<64>(a, s) : hlm::launch_fwd<128>(a, s);
   if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return HLM_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int T, int H,
+                 int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides, int window, float scale,
+                 void* stream) {
+  return run_fwd(q, k, v, o, lse, nullptr, 1, B, T, H, Hkv, D, q_strides, k_strides, v_strides, o_strides, window,
+                 scale, stream);
+}
+
+int hlm_attn_fwd_split_count(int B, int T, int H, int D, int window) {
+  if (B <= 0 || T <= 0 || H <= 0 || (D != 64 && D != 128)) return 1;
+  const int W = effective_window(window, T);
+  return D == 64 ? hlm::fwd_split_count<64>(B, T, H, W) : hlm::fwd_split_count<128>(B, T, H, W);
+}
+
+int hlm_attn_fwd_split(const void* q, const void* k, const void* v, void* o, float* lse, float* ws, int nsplit,
+                       int B, int T, int H, int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides, int window, float scale,
+                       void* stream) {
+  return run_fwd(q, k, v, o, lse, ws, nsplit, B, T, H, Hkv, D, q_strides, k_strides, v_strides, o_strides, window,
+                 scale, stream);
 }
 
 }  // extern "C"

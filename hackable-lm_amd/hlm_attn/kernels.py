@@ -66,14 +66,20 @@ def attention(
     keys i-W+1..i.  Differentiable in q, k and v."""
     from . import ops  # registers the custom ops on first use
 
-    q = q.to(torch.bfloat16)
-    k = k.to(torch.bfloat16)
-    v = v.to(torch.bfloat16)
+    if q.dtype != torch.bfloat16:
+        q = q.to(torch.bfloat16)
+    if k.dtype != torch.bfloat16:
+        k = k.to(torch.bfloat16)
+    if v.dtype != torch.bfloat16:
+        v = v.to(torch.bfloat16)
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     if window_size is not None and window_size < 1:
         raise RuntimeError(f"window_size must be >= 1 or None, got {window_size}")
     window = 0 if window_size is None else int(window_size)
+    if ops.direct_call_ok(q, k, v):  # inference: same kernels, without the dispatcher's host cost
+        out, _ = ops.attn_fwd_impl(q, k, v, window, float(scale))
+        return out
     out, _ = ops.hip_attn_fwd(q, k, v, window, float(scale))
     return out
 
@@ -123,4 +129,6 @@ def qk_norm_rope_hip(
 
     if q.device.type != "cuda":
         raise RuntimeError("qk_norm_rope_hip runs on ROCm devices only; use the torch path on the CPU")
+    if ops.direct_call_ok(q, k, cos, sin):  # inference: same kernel, without the dispatcher's host cost
+        return ops.qk_norm_rope_impl(q, k, cos, sin, float(eps))
     return ops.hip_qk_norm_rope(q, k, cos, sin, float(eps))

@@ -12,6 +12,7 @@ ROCm device, or without libhlm_attn.so, the ops raise.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -35,15 +36,17 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
 
 
 def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
-    if q.device.type != "cuda":
-        raise RuntimeError(f"hip attention runs on ROCm devices only, got a tensor on {q.device}")
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        if t.dtype != _BF16:
-            raise RuntimeError(f"hip attention expects bfloat16 {name}, got {t.dtype}")
-        if t.dim() != 4:
-            raise RuntimeError(f"hip attention expects {name} shaped (B, T, H, D), got {tuple(t.shape)}")
-        if t.device != q.device:
-            raise RuntimeError("q, k and v must be on the same device")
+    dev = q.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"hip attention runs on ROCm devices only, got a tensor on {dev}")
+    if not (q.dtype == k.dtype == v.dtype == _BF16 and q.dim() == k.dim() == v.dim() == 4
+            and k.device == dev and v.device == dev):
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if t.dtype != _BF16:
+                raise RuntimeError(f"hip attention expects bfloat16 {name}, got {t.dtype}")
+            if t.dim() != 4:
+                raise RuntimeError(f"hip attention expects {name} shaped (B, T, H, D), got {tuple(t.shape)}")
+        raise RuntimeError("q, k and v must be on the same device")
     if k.shape != v.shape:
         raise RuntimeError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must have the same shape")
     if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
@@ -52,29 +55,87 @@ def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise RuntimeError(f"query heads {q.shape[2]} are not a multiple of kv heads {k.shape[2]}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(device: torch.device) -> ctypes.c_void_p:
+    """torch's current stream on `device` (a capture stream inside graph
+    capture), as the hipStream_t the kernels launch on."""
+    if _raw_stream is not None:  # the same handle without building a Stream object
+        return ctypes.c_void_p(_raw_stream(device.index if device.index is not None else torch.cuda.current_device()))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-@torch.library.custom_op("hackable_lm::hip_attn_fwd", mutates_args=())
-def hip_attn_fwd(
+def _on_device(device: torch.device):
+    """Makes `device` current for the launch; a no-op (and no device guard's
+    cost) when it already is."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
+def direct_call_ok(*tensors: torch.Tensor) -> bool:
+    """True when a call may skip torch's op dispatcher and run the kernels'
+    Python implementation directly: plain tensors (not fake or traced), no
+    torch.compile tracing in progress, and no input that needs a gradient
+    (inference, e.g. the evaluation harness's no-grad forwards).  The
+    dispatcher and autograd wrapper cost far more host time than the launch."""
+    if torch.compiler.is_compiling():
+        return False
+    grad = torch.is_grad_enabled()
+    for t in tensors:
+        if type(t) is not torch.Tensor or (grad and t.requires_grad):
+            return False
+    return True
+
+
+def attn_fwd_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The forward launch behind hackable_lm::hip_attn_fwd (o, lse)."""
     _check_inputs(q, k, v)
     lib = _lib.load()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     B, T, H, D = q.shape
     o = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
-        rc = lib.hlm_attn_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-            B, T, H, k.shape[2], D,
-            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o),
-            int(window), float(scale), _stream_handle(q.device),
-        )
+    nsplit = split_count(lib, B, T, H, D, int(window))
+    strides = (_lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o))
+    with _on_device(q.device):
+        if nsplit > 1:  # small grid: split each query tile's keys, then merge (evaluation-sized calls)
+            ws = torch.empty(nsplit * B * H * T * (D + 2), dtype=torch.float32, device=q.device)
+            rc = lib.hlm_attn_fwd_split(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), ws.data_ptr(), nsplit,
+                B, T, H, k.shape[2], D, *strides, int(window), float(scale), _stream_handle(q.device),
+            )
+        else:
+            rc = lib.hlm_attn_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                B, T, H, k.shape[2], D, *strides, int(window), float(scale), _stream_handle(q.device),
+            )
     _lib.check(rc, lib)
     return o, lse
+
+
+_split_cache: dict = {}
+
+
+def split_count(lib, B: int, T: int, H: int, D: int, window: int) -> int:
+    """hlm_attn_fwd_split_count, memoised per shape."""
+    key = (B, T, H, D, window)
+    n = _split_cache.get(key)
+    if n is None:
+        if len(_split_cache) > 4096:
+            _split_cache.clear()
+        n = _split_cache[key] = lib.hlm_attn_fwd_split_count(B, T, H, D, window)
+    return n
+
+
+@torch.library.custom_op("hackable_lm::hip_attn_fwd", mutates_args=())
+def hip_attn_fwd(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    return attn_fwd_impl(q, k, v, window, scale)
 
 
 @hip_attn_fwd.register_fake
@@ -108,7 +169,7 @@ def hip_attn_bwd(
     dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     dv = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # -lse*log2(e), -rowsum(dO*O)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         rc = lib.hlm_attn_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
@@ -188,10 +249,10 @@ def _check_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor) -> None:
         raise RuntimeError("q, k, cos and sin must be on the same device")
 
 
-@torch.library.custom_op("hackable_lm::hip_qk_norm_rope", mutates_args=())
-def hip_qk_norm_rope(
+def qk_norm_rope_impl(
     q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The forward launch behind hackable_lm::hip_qk_norm_rope."""
     _check_qk(q, k, cos)
     lib = _lib.load()
     q, k = _kernel_ready(q), _kernel_ready(k)
@@ -201,7 +262,7 @@ def hip_qk_norm_rope(
     s, _ = _rope_table(sin.to(c.dtype), T)
     q_out = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
     k_out = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         rc = lib.hlm_qk_norm_rope_fwd(
             q.data_ptr(), k.data_ptr(), c.data_ptr(), s.data_ptr(), code, q_out.data_ptr(), k_out.data_ptr(),
             B, T, H, Hkv, D, c.shape[1], _lib.strides3(q), _lib.strides3(k), float(eps),
@@ -209,6 +270,13 @@ def hip_qk_norm_rope(
         )
     _lib.check(rc, lib)
     return q_out, k_out
+
+
+@torch.library.custom_op("hackable_lm::hip_qk_norm_rope", mutates_args=())
+def hip_qk_norm_rope(
+    q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    return qk_norm_rope_impl(q, k, cos, sin, eps)
 
 
 @hip_qk_norm_rope.register_fake
@@ -237,7 +305,7 @@ def hip_qk_norm_rope_backward(
     s, _ = _rope_table(sin.to(c.dtype), T)
     dq = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
     dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         rc = lib.hlm_qk_norm_rope_bwd(
             q.data_ptr(), k.data_ptr(), gq.data_ptr(), gk.data_ptr(), c.data_ptr(), s.data_ptr(), code,
             dq.data_ptr(), dk.data_ptr(), B, T, H, Hkv, D, c.shape[1],

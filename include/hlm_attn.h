@@ -48,6 +48,9 @@ extern "C" {
 #define HLM_ATTN_EUNSUPPORTED (-2) /* valid request this library does not implement */
 #define HLM_ATTN_ELAUNCH (-3)     /* the HIP runtime rejected a kernel launch */
 
+/* Largest nsplit hlm_attn_fwd_split accepts. */
+#define HLM_ATTN_MAX_SPLIT 16
+
 /* Element types of the rotary tables (cos, sin) of hlm_qk_norm_rope_*. */
 #define HLM_TABLE_F32 0
 #define HLM_TABLE_BF16 1
@@ -67,6 +70,34 @@ int hlm_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
                  const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides,
                  int window, float scale, void* stream);
+
+/*
+ * Split-key forward for small grids (the evaluation harness's calls at batch
+ * 1 and ragged T, lm_eval_hackable_lm.py:134-160,185-207, where B * H * T/128
+ * query tiles leave most of the chip idle and the longest row's key tiles set
+ * the time).  Same inputs, outputs and semantics as hlm_attn_fwd; nsplit
+ * workgroups share each query tile's key range and a second kernel merges
+ * their partial results by their log-sum-exp.  ws is caller-allocated device
+ * memory of nsplit * B * H * T * (D + 2) floats, 16-byte aligned (fully
+ * overwritten; no initialisation needed); nsplit in [1, HLM_ATTN_MAX_SPLIT]
+ * (1 is hlm_attn_fwd, and ws may then be null).  Results agree with
+ * hlm_attn_fwd within bf16 rounding of O (the partial sums are fp32).  No
+ * counterpart in the reference: FlashAttention-2's forward is one call.
+ */
+int hlm_attn_fwd_split(const void* q, const void* k, const void* v, void* o, float* lse, float* ws, int nsplit,
+                       int B, int T, int H, int Hkv, int D, const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides, int window, float scale,
+                       void* stream);
+
+/*
+ * The nsplit this library recommends for hlm_attn_fwd_split on an MI355X:
+ * 1 (use hlm_attn_fwd) unless the query tiles fill less than half of the
+ * chip's workgroup slots and the longest row spans at least 24 key tiles of
+ * 64 (shorter rows run faster unsplit than split and merged); then one split
+ * per 12 key tiles of the longest row.  Pure function of the shape; touches
+ * no device.
+ */
+int hlm_attn_fwd_split_count(int B, int T, int H, int D, int window);
 
 /*
  * Backward: given dO and the forward's o and lse, writes dq, dk, dv (in the

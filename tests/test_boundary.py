@@ -92,6 +92,34 @@ def test_bwd_phases_validate_like_bwd():
         assert rc == -2
 
 
+def test_split_forward_validates_and_its_policy_targets_small_grids():
+    lib = _lib.load()
+    s = _strides(2048, 128, 64)
+    p = ctypes.c_void_p(0x1000)
+    lse = ctypes.c_void_p(0x2000)
+
+    def split(ws, nsplit, B=1):
+        return lib.hlm_attn_fwd_split(p, p, p, p, lse, ws, nsplit, B, 16, 2, 2, 64, s, s, s, s, 0, 0.125, None)
+
+    for nsplit in (0, 17):
+        assert split(ctypes.c_void_p(0x3000), nsplit) == -1
+        assert b"nsplit" in lib.hlm_attn_last_error()
+    assert split(None, 2) == -1 and b"workspace" in lib.hlm_attn_last_error()
+    assert split(ctypes.c_void_p(0x3008), 2) == -1
+    assert split(None, 1, B=0) == 0 and split(ctypes.c_void_p(0x3000), 4, B=0) == 0
+    # the policy: the training shape is a full grid; batch-1 evaluation calls split
+    count = lib.hlm_attn_fwd_split_count
+    assert count(8, 2048, 12, 64, 512) == 1
+    assert count(1, 2048, 12, 64, 0) == 2  # 33 key tiles in the longest row
+    assert count(1, 2048, 12, 64, 512) == 1 and count(1, 1024, 12, 64, 0) == 1  # rows too short to pay
+    assert count(1, 8192, 1, 64, 0) == 10  # 129 key tiles; slots allow 12
+    assert count(1, 16384, 1, 128, 0) == 4  # bounded by the 512 slots of D = 128
+    assert count(1, 128, 12, 64, 0) == 1
+    assert count(1, 2048, 12, 96, 0) == 1 and count(0, 2048, 12, 64, 0) == 1
+    for B, T, H in ((1, 5000, 1), (1, 16384, 2), (2, 700, 3)):
+        assert 1 <= count(B, T, H, 128, 0) <= 16
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_lib.HipAttentionUnavailable, match="build it"):
         _lib.load(tmp_path / "libhlm_attn.so")
@@ -145,8 +173,26 @@ class FakeOp:
 @pytest.fixture()
 def fake_op(monkeypatch):
     fake = FakeOp()
-    monkeypatch.setattr(ops, "hip_attn_fwd", fake)
+    monkeypatch.setattr(ops, "hip_attn_fwd", fake)  # the custom op (autograd / torch.compile)
+    monkeypatch.setattr(ops, "attn_fwd_impl", fake)  # the direct inference path
     return fake
+
+
+def test_direct_path_only_for_plain_inference_calls():
+    """Calls skip the dispatcher only when nothing needs autograd or tracing."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    q = torch.randn(1, 4, 2, 64)
+    assert ops.direct_call_ok(q, q, q)
+    w = q.clone().requires_grad_(True)
+    assert not ops.direct_call_ok(q, w, q)
+    with torch.no_grad():
+        assert ops.direct_call_ok(q, w, q)
+    with torch.inference_mode():
+        assert ops.direct_call_ok(q, q, q)
+    with FakeTensorMode():
+        f = torch.empty(1, 4, 2, 64)
+        assert not ops.direct_call_ok(f, f, f)
 
 
 def test_sdpa_casts_to_bf16_and_maps_window(fake_op):
