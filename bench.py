@@ -16,7 +16,8 @@ MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
 A "producer" object times the q/k RMSNorm + partial RoPE kernels that feed
 attention (forward and backward) at cfg2's q/k shape against the HBM roofline;
 an "eval" object times the evaluation harness's no-grad forwards at batch 1
-and ragged T.
+and ragged T; an "lm_head" object times the LM head's cross-entropy rows
+against the HBM roofline.
 
 Steps are eager launches by default (they run ahead of the GPU); --graph times
 HIP-graph replays of one captured step instead (the way a training step runs
@@ -24,7 +25,7 @@ under torch.compile's CUDA-graph mode).  The default warmup (300 steps) lets
 the GPU reach its steady clock before timing starts.
 
   python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline] [--graph]
-                  [--no-producer] [--no-eval]
+                  [--no-producer] [--no-eval] [--no-lm-head]
 """
 from __future__ import annotations
 
@@ -243,6 +244,54 @@ def measure_producer(reps: int, warmup: int, device) -> dict:
             "traffic": read_traffic("producer_cfg2", f"qk_norm_rope_{name}"),
         }
     return out
+
+
+LM_HEAD_CONFIG = dict(rows=4096, V=32768)  # loss_chunk_size 4096 (config.py:49), the Triton kernel's largest V
+
+
+def measure_lm_head(reps: int, warmup: int, device) -> dict:
+    """HIP-event launch time of the LM head's cross-entropy rows (hlm_ce_rows)
+    on one chunk of bf16 logits, against the HBM roofline: 2 * rows * V * 2
+    bytes (each logit read once, its gradient written once) plus the targets
+    and losses.  Launches alternate between two chunks (537 MB together,
+    beyond the 256 MB last-level cache), so the logits come from HBM."""
+    import torch
+
+    from hlm_attn import _lib
+
+    lib = _lib.load()
+    rows, V = LM_HEAD_CONFIG["rows"], LM_HEAD_CONFIG["V"]
+    g = torch.Generator(device="cpu").manual_seed(0)
+    bufs = [(torch.randn(rows, V, generator=g) * 3).to(torch.bfloat16).to(device) for _ in range(2)]
+    targets = torch.randint(0, V, (rows,), generator=g).to(device)
+    loss = torch.empty(rows, dtype=torch.float32, device=device)
+    it = [0]
+
+    def launch():
+        buf = bufs[it[0]]
+        it[0] ^= 1
+        rc = lib.hlm_ce_rows(buf.data_ptr(), _lib.DTYPE_BF16, V, targets.data_ptr(), loss.data_ptr(), rows, V,
+                             rows, -100, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+        assert rc == 0, lib.hlm_attn_last_error()
+
+    for _ in range(warmup):
+        launch()
+    ms = event_time_ms(torch, launch, reps)
+    nbytes = 2 * rows * V * 2 + rows * 12
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "op": "LM-head cross-entropy rows, in place (kernels.py:286-336 inside :878-959)",
+        "workload": f"rows={rows} V={V} bf16 logits (one loss chunk), random targets",
+        "kernel": "ce_rows_vec_kernel<bf16, 16>",
+        "bound": "hbm",
+        "launch_us": round(ms * 1e3, 2),
+        "algorithmic_bytes_per_launch": nbytes,
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": read_traffic("lm_head_ce", "ce_rows_vec_kernel"),
+    }
 
 
 EVAL_SHAPES = ((1, 128), (1, 512), (1, 1024), (1, 2048), (8, 2048))  # (B, T) at H=12, D=64
@@ -466,6 +515,7 @@ def main() -> int:
     ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step instead of eager launches")
     ap.add_argument("--no-producer", action="store_true", help="skip the q/k RMSNorm + RoPE producer's timing")
     ap.add_argument("--no-eval", action="store_true", help="skip the evaluation-path (no-grad, batch 1) timings")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the LM-head cross-entropy timing")
     ap.add_argument(
         "--copy-mib", type=int, default=0,
         help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
@@ -546,6 +596,8 @@ def main() -> int:
         line["producer"] = measure_producer(max(args.steps, 50), 20, device)
     if not args.no_eval:
         line["eval"] = measure_eval(max(args.steps // 2, 50), device)
+    if not args.no_lm_head:
+        line["lm_head"] = measure_lm_head(max(args.steps // 4, 20), 5, device)
     print(json.dumps(line), flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4

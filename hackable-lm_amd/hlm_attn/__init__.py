@@ -8,6 +8,8 @@ Public surface:
   ATTENTION_BACKENDS, layer_attention_window  config.py's names and layer pattern
   hip_attention_available, resolve_attention_backend
   qk_norm_rope_hip                            the fused q/k RMSNorm + partial RoPE producer
+  fused_linear_cross_entropy_with_weight      the LM head's chunked linear + cross-entropy (backend="hip")
+  LMHeadProjection                            model.py's LM head with fwd_hip
 The kernels live in libhlm_attn.so (built by hlm_attn.build), reached through
 the C ABI in include/hlm_attn.h.
 """
@@ -24,12 +26,13 @@ from .config import (
 )
 from .kernels import (
     attention,
+    fused_linear_cross_entropy_with_weight,
     hip_attention_available,
     qk_norm_rope_hip,
     resolve_attention_backend,
     scaled_dot_product_attention,
 )
-from .model import AttentionConfig, AttentionCore, QKVProjection, RotaryEmbedding
+from .model import AttentionConfig, AttentionCore, LMHeadProjection, QKVProjection, RotaryEmbedding
 
 __all__ = [
     "ATTENTION_BACKENDS",
@@ -38,6 +41,8 @@ __all__ = [
     "AttentionConfig",
     "AttentionCore",
     "attention",
+    "fused_linear_cross_entropy_with_weight",
+    "LMHeadProjection",
     "attention_window_size",
     "hip_attention_available",
     "layer_attention_window",

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -29,6 +29,9 @@ SIGNATURES["hlm_attn_fwd_split_count"] = (_I, [_I, _I, _I, _I, _I])
 SIGNATURES["hlm_qk_norm_rope_fwd"] = (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
 SIGNATURES["hlm_qk_norm_rope_bwd"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])
 TABLE_F32, TABLE_BF16 = 0, 1  # HLM_TABLE_F32 / HLM_TABLE_BF16
+DTYPE_F32, DTYPE_BF16 = 0, 1  # HLM_DTYPE_F32 / HLM_DTYPE_BF16
+_I64 = ctypes.c_int64
+SIGNATURES["hlm_ce_rows"] = (_I, [_P, _I, _I64, _P, _P, _I, _I, _I64, _I, _P])
 
 _lib: ctypes.CDLL | None = None
 

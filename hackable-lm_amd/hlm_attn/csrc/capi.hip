@@ -17,6 +17,8 @@ template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases);
 template <int D>
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream);
+hipError_t launch_ce_rows(void* logits, bool bf16_logits, int64_t row_stride, const int64_t* targets, float* loss,
+                          int n_rows, int V, float inv_n, int ignore_index, hipStream_t stream);
 }  // namespace hlm
 
 namespace {
@@ -74,7 +76,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 4; }
+int hlm_attn_abi_version(void) { return 5; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -292,6 +294,24 @@ int hlm_qk_norm_rope_bwd(const void* q, const void* k, const void* grad_q_out, c
                          const int64_t* k_strides, float eps, void* stream) {
   return run_qk_norm_rope(true, q, k, grad_q_out, grad_k_out, cos, sin, table_dtype, grad_q, grad_k, B, T, H, Hkv,
                           D, rotary_dim, q_strides, k_strides, eps, stream);
+}
+
+int hlm_ce_rows(void* logits, int logits_dtype, int64_t row_stride, const int64_t* targets, float* loss, int n_rows,
+                int n_cols, int64_t n_tokens, int ignore_index, void* stream) {
+  g_last_error[0] = '\0';
+  if (n_rows < 0 || n_cols <= 0) return fail(HLM_ATTN_EINVAL, "bad shape n_rows=%d n_cols=%d", n_rows, n_cols);
+  if (logits_dtype != HLM_DTYPE_F32 && logits_dtype != HLM_DTYPE_BF16)
+    return fail(HLM_ATTN_EINVAL, "logits_dtype %d is neither HLM_DTYPE_F32 nor HLM_DTYPE_BF16", logits_dtype);
+  if (row_stride < n_cols) return fail(HLM_ATTN_EINVAL, "row_stride %lld is below n_cols %d", (long long)row_stride, n_cols);
+  if (n_tokens <= 0) return fail(HLM_ATTN_EINVAL, "n_tokens must be positive");
+  if (n_rows == 0) return HLM_ATTN_OK;
+  if (logits == nullptr || targets == nullptr || loss == nullptr)
+    return fail(HLM_ATTN_EINVAL, "logits, targets or loss is a null pointer");
+  const hipError_t err = hlm::launch_ce_rows(logits, logits_dtype == HLM_DTYPE_BF16, row_stride, targets, loss, n_rows,
+                                             n_cols, (float)(1.0 / (double)n_tokens), ignore_index,
+                                             static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "cross-entropy launch failed: %s", hipGetErrorString(err));
+  return HLM_ATTN_OK;
 }
 
 }  // extern "C"

@@ -14,6 +14,10 @@ attention field.
 `qk_norm_rope_hip` is the producer step before attention, with the signature
 and semantics of the reference's `qk_norm_rope_triton` (kernels.py:756-771):
 RMSNorm of each q and k row, then the partial rotary embedding.
+
+`fused_linear_cross_entropy_with_weight(..., backend="hip")` is the LM head's
+chunked linear + cross-entropy (kernels.py:878-959) with the HIP
+cross-entropy rows in place of the Triton `linear_ce` op.
 """
 from __future__ import annotations
 
@@ -132,3 +136,105 @@ def qk_norm_rope_hip(
     if ops.direct_call_ok(q, k, cos, sin):  # inference: same kernel, without the dispatcher's host cost
         return ops.qk_norm_rope_impl(q, k, cos, sin, float(eps))
     return ops.hip_qk_norm_rope(q, k, cos, sin, float(eps))
+
+
+# --- the LM head's fused linear + cross-entropy -----------------------------------
+
+LINEAR_CE_MIN_CHUNK_SIZE = 2048  # kernels.py:252
+
+
+def _next_power_of_2(n: int) -> int:
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+def linear_ce_chunk_size(n_tokens: int, hidden_size: int, vocab_size: int, requested: int | None) -> int:
+    """Rows per chunk, by the reference's rule (kernels.py:897-903): a requested
+    size (at least 2048), or enough rows that one chunk's logits are about the
+    size of the hidden states; never more than n_tokens."""
+    if requested is not None and requested < 0:
+        raise RuntimeError(f"loss_chunk_size must be nonnegative, got {requested}")
+    if requested:
+        return min(n_tokens, max(requested, LINEAR_CE_MIN_CHUNK_SIZE))
+    inc_factor = -(-vocab_size // hidden_size)
+    chunk = _next_power_of_2(-(-n_tokens // inc_factor))
+    return min(n_tokens, max(chunk, LINEAR_CE_MIN_CHUNK_SIZE))
+
+
+class _HipFusedLinearCrossEntropy(torch.autograd.Function):
+    """kernels.py:878-942 with the HIP cross-entropy rows: per chunk of rows,
+    logits = hidden @ W^T (+ b) by the library GEMM, the HIP kernel turns them
+    into per-row losses and, in place, the gradient of the mean loss, and
+    the gradients of hidden, W and b are accumulated from it in the forward;
+    the backward scales them by the incoming gradient."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, targets, bias, requested_chunk_size):
+        from . import ops
+
+        hidden = hidden.contiguous()
+        weight = weight.contiguous()
+        targets = targets.contiguous()
+        n_tokens, hidden_size = hidden.shape
+        vocab_size = weight.shape[0]
+        chunk_size = linear_ce_chunk_size(n_tokens, hidden_size, vocab_size, requested_chunk_size)
+        grad_hidden = torch.empty_like(hidden)
+        grad_weight = torch.zeros_like(weight) if weight.requires_grad else None
+        grad_bias = torch.zeros_like(bias) if bias is not None and bias.requires_grad else None
+        loss_1d = torch.empty(n_tokens, dtype=torch.float32, device=hidden.device)
+        for start in range(0, n_tokens, chunk_size):
+            end = min(start + chunk_size, n_tokens)
+            hidden_chunk = hidden[start:end]
+            logits = hidden_chunk @ weight.t()
+            if bias is not None:
+                logits = logits + bias
+            logits = logits.contiguous()
+            loss_1d[start:end] = ops.hip_linear_ce(logits, targets[start:end], n_tokens)
+            grad_logits = logits
+            if hidden.requires_grad:
+                grad_hidden[start:end] = grad_logits @ weight
+            if grad_weight is not None:
+                grad_weight += torch.mm(grad_logits.t(), hidden_chunk).to(grad_weight.dtype)
+            if grad_bias is not None:
+                grad_bias += grad_logits.sum(dim=0).to(grad_bias.dtype)
+        ctx.save_for_backward(
+            grad_hidden.detach() if hidden.requires_grad else None,
+            grad_weight.detach() if grad_weight is not None else None,
+            grad_bias.detach() if grad_bias is not None else None,
+        )
+        return loss_1d.sum()
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        grad_hidden, grad_weight, grad_bias = ctx.saved_tensors
+
+        def scaled(g):
+            return None if g is None else g * grad_output.to(dtype=g.dtype)
+
+        return (
+            scaled(grad_hidden) if ctx.needs_input_grad[0] else None,
+            scaled(grad_weight) if ctx.needs_input_grad[1] else None,
+            None,
+            scaled(grad_bias) if ctx.needs_input_grad[3] else None,
+            None,
+        )
+
+
+def fused_linear_cross_entropy_with_weight(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    targets: torch.Tensor,
+    backend: str = HIP_BACKEND,
+    chunk_size: int | None = None,
+) -> torch.Tensor:
+    """The reference's entry (kernels.py:945-959) with backend="hip": the mean
+    cross-entropy of hidden @ W^T (+ b) against targets, differentiable in
+    hidden, W and b.  There is no CPU path (the reference's own torch branch
+    serves CPU tensors)."""
+    if backend != HIP_BACKEND:
+        raise RuntimeError(f"unsupported fused linear cross entropy backend {backend!r}")
+    hidden_flat = hidden.reshape(-1, hidden.size(-1))
+    targets_flat = targets.reshape(-1).contiguous()
+    if hidden_flat.device.type != "cuda":
+        raise RuntimeError("the hip fused linear cross entropy runs on ROCm devices only")
+    return _HipFusedLinearCrossEntropy.apply(hidden_flat, weight, targets_flat, bias, chunk_size)

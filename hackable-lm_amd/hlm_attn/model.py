@@ -1,5 +1,5 @@
-"""AttentionCore and QKVProjection with the hip backend, mirroring
-hackable-lm's model.py:129-250 and model.py:50-126.
+"""AttentionCore, QKVProjection and LMHeadProjection with the hip backend,
+mirroring hackable-lm's model.py:129-250, model.py:50-126 and model.py:317-352.
 
 The reference picks `fwd_<attention_backend>` per call (model.py:169-174);
 this class carries the same per-layer window (model.py:136), the same
@@ -49,6 +49,10 @@ class AttentionConfig:
     rope_fraction: float = 0.25
     norm_eps: float = 1e-6
     qkv_backend: str = "hip"
+    # LMHeadProjection's fields (config.py:213-232)
+    vocab_size: int = 0
+    loss_chunk_size: int | None = 4096
+    lm_head_backend: str = "hip"
 
 
 class RotaryEmbedding(nn.Module):
@@ -148,3 +152,30 @@ class AttentionCore(nn.Module):
             window_size=self._attention_window_size(q.shape[1]),
             backend="hip",
         )
+
+
+class LMHeadProjection(nn.Module):
+    """model.py:317-352 with the hip fused linear + cross-entropy: without
+    targets the logits; with targets (None, mean loss) through
+    kernels.fused_linear_cross_entropy_with_weight(backend="hip")."""
+
+    def __init__(self, config: AttentionConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.lm_head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self.chunk_size = config.loss_chunk_size
+
+    def forward(self, hidden: torch.Tensor, targets: torch.Tensor | None = None):
+        backend = normalize_module_backend("lm_head_backend", self.config.lm_head_backend)
+        fwd_backend = getattr(self, f"fwd_{backend}", None)
+        if fwd_backend is None:
+            raise RuntimeError(f"{type(self).__name__} does not support backend {backend!r}")
+        return fwd_backend(hidden, targets)
+
+    def fwd_hip(self, hidden: torch.Tensor, targets: torch.Tensor | None = None):
+        if targets is None:
+            return self.lm_head(hidden), None
+        loss = kernels.fused_linear_cross_entropy_with_weight(
+            hidden, self.lm_head.weight, self.lm_head.bias, targets, backend="hip", chunk_size=self.chunk_size
+        )
+        return None, loss

@@ -337,3 +337,46 @@ def _qk_backward(ctx, grad_q, grad_k):
 
 
 hip_qk_norm_rope.register_autograd(_qk_backward, setup_context=_qk_setup_context)
+
+
+# --- the LM head: cross-entropy rows of the fused linear + cross-entropy ----------
+#
+# hackable_lm::hip_linear_ce mirrors the reference's Triton op
+# hackable_lm::linear_ce (/root/reference/kernels.py:320-336): it overwrites
+# `logits` in place with the gradient of the mean loss and returns the
+# per-row losses (already divided by n_tokens).
+
+IGNORE_INDEX = -100  # F.cross_entropy's default ignore_index
+
+
+def linear_ce_impl(logits: torch.Tensor, targets: torch.Tensor, n_tokens: int) -> torch.Tensor:
+    """The launch behind hackable_lm::hip_linear_ce."""
+    if logits.device.type != "cuda":
+        raise RuntimeError(f"hip linear_ce runs on ROCm devices only, got a tensor on {logits.device}")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise RuntimeError(f"hip linear_ce expects (rows, vocab) logits with unit column stride, got {tuple(logits.shape)}")
+    if logits.dtype not in (_BF16, torch.float32):
+        raise RuntimeError(f"hip linear_ce expects bfloat16 or float32 logits, got {logits.dtype}")
+    if targets.shape != (logits.shape[0],):
+        raise RuntimeError(f"targets {tuple(targets.shape)} do not match {logits.shape[0]} logit rows")
+    lib = _lib.load()
+    targets = targets.to(device=logits.device, dtype=torch.int64).contiguous()
+    loss = torch.empty(logits.shape[0], dtype=torch.float32, device=logits.device)
+    code = _lib.DTYPE_BF16 if logits.dtype == _BF16 else _lib.DTYPE_F32
+    with _on_device(logits.device):
+        rc = lib.hlm_ce_rows(
+            logits.data_ptr(), code, logits.stride(0), targets.data_ptr(), loss.data_ptr(),
+            logits.shape[0], logits.shape[1], int(n_tokens), IGNORE_INDEX, _stream_handle(logits.device),
+        )
+    _lib.check(rc, lib)
+    return loss
+
+
+@torch.library.custom_op("hackable_lm::hip_linear_ce", mutates_args=("logits",))
+def hip_linear_ce(logits: torch.Tensor, targets: torch.Tensor, n_tokens: int) -> torch.Tensor:
+    return linear_ce_impl(logits, targets, n_tokens)
+
+
+@hip_linear_ce.register_fake
+def _(logits, targets, n_tokens):
+    return logits.new_empty((logits.shape[0],), dtype=torch.float32)

@@ -55,6 +55,10 @@ extern "C" {
 #define HLM_TABLE_F32 0
 #define HLM_TABLE_BF16 1
 
+/* Element types of hlm_ce_rows' logits (the same codes). */
+#define HLM_DTYPE_F32 0
+#define HLM_DTYPE_BF16 1
+
 /* ABI revision of this header; bumped on any signature change. */
 int hlm_attn_abi_version(void);
 
@@ -174,6 +178,24 @@ int hlm_qk_norm_rope_bwd(const void* q, const void* k, const void* grad_q_out, c
                          const void* cos, const void* sin, int table_dtype, void* grad_q, void* grad_k,
                          int B, int T, int H, int Hkv, int D, int rotary_dim,
                          const int64_t* q_strides, const int64_t* k_strides, float eps, void* stream);
+
+/*
+ * The cross-entropy rows of the LM head's fused linear + cross-entropy, in
+ * place: for each of n_rows rows of n_cols logits (bf16 or fp32 per
+ * logits_dtype, rows row_stride elements apart) and its int64 target t,
+ *   loss[row] = (logsumexp(x) - x_t) / n_tokens            (fp32)
+ *   x_j      <- (softmax(x)_j - [j == t]) / n_tokens        (the gradient of
+ *                                                           the mean loss)
+ * computed in fp32.  A target equal to ignore_index gives a zero loss and a
+ * zero gradient row (F.cross_entropy's rule); any other target outside
+ * [0, n_cols) gives NaN for that row.  16-byte aligned rows (logits, n_cols
+ * and row_stride multiples of 16 bytes) take a path that reads and writes
+ * each row once.  Replaces the hackable_lm::linear_ce Triton op and its
+ * kernel (/root/reference/kernels.py:286-336) inside the chunked fused
+ * linear cross-entropy (/root/reference/kernels.py:878-959).
+ */
+int hlm_ce_rows(void* logits, int logits_dtype, int64_t row_stride, const int64_t* targets, float* loss, int n_rows,
+                int n_cols, int64_t n_tokens, int ignore_index, void* stream);
 
 /* Message describing the last failed call on this thread ("" if none). */
 const char* hlm_attn_last_error(void);

@@ -26,7 +26,7 @@ HEADER = REPO / "include" / "hlm_attn.h"
 
 def declared_symbols() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(hlm_(?:attn|qk)_\w+)\s*\(", text))
+    return set(re.findall(r"\b(hlm_(?:attn|qk|ce)_\w+)\s*\(", text))
 
 
 # --- the shared library -------------------------------------------------------
@@ -417,3 +417,48 @@ def test_qkv_projection_dispatches_on_qkv_backend():
             model.QKVProjection(cfg_b, 0)(torch.randn(1, 4, 32))
     assert config.MODULE_BACKENDS == {"torch", "triton", "hip"}
     assert config.normalize_module_backend("qkv_backend", "HIP") == "hip"
+
+
+# --- LM head: cross-entropy rows -------------------------------------------------
+
+def test_ce_rows_validates_before_touching_the_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+
+    def ce(dtype=_lib.DTYPE_BF16, stride=64, rows=4, cols=64, n_tokens=4, logits=p, targets=p, loss=p):
+        return lib.hlm_ce_rows(logits, dtype, stride, targets, loss, rows, cols, n_tokens, -100, None)
+
+    for kwargs, msg in ((dict(dtype=3), b"logits_dtype"), (dict(stride=32), b"row_stride"),
+                        (dict(cols=0), b"bad shape"), (dict(n_tokens=0), b"n_tokens"),
+                        (dict(logits=None), b"null"), (dict(loss=None), b"null")):
+        assert ce(**kwargs) == -1, kwargs
+        assert msg in lib.hlm_attn_last_error(), kwargs
+    assert ce(rows=0, logits=None) == 0
+
+
+def test_linear_ce_chunk_size_follows_the_reference_rule():
+    """kernels.py:893-903: a requested size is raised to 2048 and capped at
+    n_tokens; otherwise next_pow2(ceil(n_tokens / ceil(V / hidden))), at least 2048."""
+    size = kernels.linear_ce_chunk_size
+    assert size(16384, 768, 32768, None) == 2048  # ceil(32768/768) = 43 -> next_pow2(382) = 512 -> raised to 2048
+    assert size(1 << 20, 768, 32768, None) == 32768  # next_pow2(ceil(2^20 / 43)) = 32768
+    assert size(1000, 768, 32768, None) == 1000
+    assert size(16384, 768, 32768, 4096) == 4096 and size(16384, 768, 32768, 100) == 2048
+    assert size(3000, 768, 32768, 4096) == 3000 and size(100, 64, 33, 0) == 100
+    with pytest.raises(RuntimeError, match="nonnegative"):
+        size(100, 64, 33, -1)
+
+
+def test_fused_linear_ce_refuses_cpu_tensors_and_other_backends():
+    h = torch.randn(4, 8)
+    w = torch.randn(5, 8)
+    t = torch.randint(0, 5, (4,))
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        kernels.fused_linear_cross_entropy_with_weight(h, w, None, t, backend="hip")
+    with pytest.raises(RuntimeError, match="unsupported fused linear cross entropy backend"):
+        kernels.fused_linear_cross_entropy_with_weight(h, w, None, t, backend="triton")
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        ops.hip_linear_ce(torch.randn(2, 8), torch.tensor([0, 1]), 2)
+    cfg = model.AttentionConfig(n_layer=1, n_head=1, n_kv_head=1, n_embd=8, vocab_size=5, lm_head_backend="torch")
+    with pytest.raises(RuntimeError, match="does not support backend"):
+        model.LMHeadProjection(cfg)(h[None], t[None])
