@@ -348,6 +348,27 @@ def event_time_ms(torch, fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def event_times_ms(torch, fn, reps: int, before=None) -> list[float]:
+    """Per-launch durations of fn by a HIP-event pair around each launch on
+    the launch stream; `before` (e.g. a cache flush) runs ahead of each start
+    event, outside the timed pair."""
+    pairs_ = []
+    for _ in range(reps):
+        if before is not None:
+            before()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        pairs_.append((start, end))
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in pairs_]
+
+
+FLUSH_MB = 512  # cold-cache policy: this many MB are written between timed launches (the MALL is 256 MB)
+
+
 def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> dict:
     """Times `steps` fwd+bwd steps after `warmup` untimed ones.  By default the
     steps are eager launches from Python (the launches run ahead of the GPU,
@@ -399,6 +420,17 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
     }
     bwd_ms = event_time_ms(torch, prob.bwd, reps)
     step_ms = event_time_ms(torch, run_step, reps)
+    # Per-launch medians, warm (back to back) and cold (a 512 MB buffer
+    # written before each launch evicts the last-level cache).
+    flush_buf = torch.empty(FLUSH_MB * (1 << 20) // 4, dtype=torch.float32, device=device)
+    flush = lambda: flush_buf.fill_(1.0)  # noqa: E731
+    med = {}
+    cold = {}
+    for k, fn in (("fwd", prob.fwd), ("bwd_dq", prob.bwd_dq), ("bwd_dkdv", prob.bwd_dkdv), ("bwd", prob.bwd),
+                  ("fwd_bwd", prob.step)):
+        med[k] = statistics.median(event_times_ms(torch, fn, max(reps, 100)))
+        cold[k] = statistics.median(event_times_ms(torch, fn, 50, before=flush))
+    del flush_buf
     fl = effective_flops(cfg)
     by = algorithmic_bytes(cfg)
     total = fl["fwd"] + fl["bwd"]
@@ -414,6 +446,8 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
         "fwd_ms": kern["fwd"],
         "bwd_ms": bwd_ms,
         "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
+        "median_us": {k: round(v * 1e3, 2) for k, v in med.items()},
+        "cold_us": {k: round(v * 1e3, 2) for k, v in cold.items()},
         "tflops": {
             "fwd": fl["fwd"] / (kern["fwd"] * 1e-3) / 1e12,
             "bwd": fl["bwd"] / (bwd_ms * 1e-3) / 1e12,
@@ -588,6 +622,13 @@ def main() -> int:
             "step": "HIP-graph replay of one fwd+bwd step" if r["graph"] else "eager launches from Python",
             "eager_wall_ms_per_step": round(r["eager_wall_ms_per_step"], 5),
             "event_ms_per_step": round(r["event_ms_per_step"], 5),
+            "cache_policy": "value and kernel_us: warm (steps back to back, means); median_us: per-launch "
+            f"medians, warm; cold_us: per-launch medians with {FLUSH_MB} MB written before each launch",
+            "median_us": r["median_us"],
+            "cold_us": r["cold_us"],
+            "cold_tflops_fwd_bwd": round(
+                (effective_flops(cfg)["fwd"] + effective_flops(cfg)["bwd"]) / (r["cold_us"]["fwd_bwd"] * 1e-6) / 1e12, 2
+            ),
         },
         "roofline": r["roofline"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
