@@ -17,7 +17,8 @@ A "producer" object times the q/k RMSNorm + partial RoPE kernels that feed
 attention (forward and backward) at cfg2's q/k shape against the HBM roofline;
 an "eval" object times the evaluation harness's no-grad forwards at batch 1
 and ragged T; an "lm_head" object times the LM head's cross-entropy rows
-against the HBM roofline.
+and a "residual_norm" object the residual add + RMSNorm, both against the
+HBM roofline.
 
 Steps are eager launches by default (they run ahead of the GPU); --graph times
 HIP-graph replays of one captured step instead (the way a training step runs
@@ -292,6 +293,66 @@ def measure_lm_head(reps: int, warmup: int, device) -> dict:
         "frac": round(achieved / PEAK_HBM_GBS, 4),
         "traffic": read_traffic("lm_head_ce", "ce_rows_vec_kernel"),
     }
+
+
+RESNORM_CONFIG = dict(rows=8 * 2048, n=768)  # cfg2's tokens at n_embd = 12 heads x 64
+
+
+def measure_residual_norm(reps: int, warmup: int, device) -> dict:
+    """HIP-event launch times of the residual add + RMSNorm forward and
+    backward (hlm_residual_rms_norm_fwd/_bwd) at cfg2's token count, against
+    the HBM roofline: forward reads residual and branch and writes out and
+    normed, backward reads out, grad_out and grad_normed and writes grad_in,
+    each 2 * rows * n bytes.  Launches rotate over 4 buffer sets (800 MB)."""
+    import torch
+
+    from hlm_attn import _lib
+
+    lib = _lib.load()
+    rows, n = RESNORM_CONFIG["rows"], RESNORM_CONFIG["n"]
+    g = torch.Generator(device="cpu").manual_seed(0)
+    sets = [[torch.randn(rows, n, generator=g).to(torch.bfloat16).to(device) for _ in range(4)] for _ in range(4)]
+    it = [0]
+
+    def nxt():
+        st = sets[it[0]]
+        it[0] = (it[0] + 1) % len(sets)
+        return st
+
+    def stream():
+        return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+    def fwd():
+        a, b, c, d = nxt()
+        assert lib.hlm_residual_rms_norm_fwd(a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), rows, n,
+                                             1e-6, stream()) == 0
+
+    def bwd():
+        a, b, c, d = nxt()
+        assert lib.hlm_residual_rms_norm_bwd(a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), rows, n,
+                                             1e-6, stream()) == 0
+
+    out = {
+        "op": "residual add + RMSNorm (model.py:73-75 in OutputProjection / DownProjection)",
+        "workload": f"rows={rows} n={n} bf16",
+        "bound": "hbm",
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+    }
+    nbytes = 4 * rows * n * 2
+    for name, fn in (("fwd", fwd), ("bwd", bwd)):
+        for _ in range(warmup):
+            fn()
+        ms = event_time_ms(torch, fn, reps)
+        achieved = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {
+            "launch_us": round(ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": nbytes,
+            "achieved": round(achieved, 1),
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": read_traffic("residual_norm", f"residual_rms_norm_{name}"),
+        }
+    return out
 
 
 EVAL_SHAPES = ((1, 128), (1, 512), (1, 1024), (1, 2048), (8, 2048))  # (B, T) at H=12, D=64
@@ -639,6 +700,7 @@ def main() -> int:
         line["eval"] = measure_eval(max(args.steps // 2, 50), device)
     if not args.no_lm_head:
         line["lm_head"] = measure_lm_head(max(args.steps // 4, 20), 5, device)
+        line["residual_norm"] = measure_residual_norm(max(args.steps // 2, 50), 10, device)
     print(json.dumps(line), flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4

@@ -10,6 +10,8 @@ Public surface:
   qk_norm_rope_hip                            the fused q/k RMSNorm + partial RoPE producer
   fused_linear_cross_entropy_with_weight      the LM head's chunked linear + cross-entropy (backend="hip")
   LMHeadProjection                            model.py's LM head with fwd_hip
+  residual_rms_norm_hip                       residual add + RMSNorm (OutputProjection / DownProjection)
+  OutputProjection, DownProjection            model.py's projections with fwd_hip
 The kernels live in libhlm_attn.so (built by hlm_attn.build), reached through
 the C ABI in include/hlm_attn.h.
 """
@@ -29,10 +31,19 @@ from .kernels import (
     fused_linear_cross_entropy_with_weight,
     hip_attention_available,
     qk_norm_rope_hip,
+    residual_rms_norm_hip,
     resolve_attention_backend,
     scaled_dot_product_attention,
 )
-from .model import AttentionConfig, AttentionCore, LMHeadProjection, QKVProjection, RotaryEmbedding
+from .model import (
+    AttentionConfig,
+    AttentionCore,
+    DownProjection,
+    LMHeadProjection,
+    OutputProjection,
+    QKVProjection,
+    RotaryEmbedding,
+)
 
 __all__ = [
     "ATTENTION_BACKENDS",
@@ -53,6 +64,9 @@ __all__ = [
     "QKVProjection",
     "RotaryEmbedding",
     "qk_norm_rope_hip",
+    "residual_rms_norm_hip",
+    "OutputProjection",
+    "DownProjection",
     "resolve_attention_backend",
     "scaled_dot_product_attention",
 ]

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -32,6 +32,8 @@ TABLE_F32, TABLE_BF16 = 0, 1  # HLM_TABLE_F32 / HLM_TABLE_BF16
 DTYPE_F32, DTYPE_BF16 = 0, 1  # HLM_DTYPE_F32 / HLM_DTYPE_BF16
 _I64 = ctypes.c_int64
 SIGNATURES["hlm_ce_rows"] = (_I, [_P, _I, _I64, _P, _P, _I, _I, _I64, _I, _P])
+SIGNATURES["hlm_residual_rms_norm_fwd"] = (_I, [_P, _P, _P, _P, _I64, _I, _F, _P])
+SIGNATURES["hlm_residual_rms_norm_bwd"] = (_I, [_P, _P, _P, _P, _I64, _I, _F, _P])
 
 _lib: ctypes.CDLL | None = None
 

@@ -14,7 +14,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libhlm_attn.so"
-SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "qk_norm_rope.hip", "linear_ce.hip", "capi.hip")
+SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code.

@@ -19,6 +19,8 @@ template <int D>
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream);
 hipError_t launch_ce_rows(void* logits, bool bf16_logits, int64_t row_stride, const int64_t* targets, float* loss,
                           int n_rows, int V, float inv_n, int ignore_index, hipStream_t stream);
+hipError_t launch_residual_rms_norm(const void* a, const void* b, const void* c, void* y0, void* y1, int64_t rows,
+                                    int n, float eps, bool backward, hipStream_t stream);
 }  // namespace hlm
 
 namespace {
@@ -76,7 +78,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 5; }
+int hlm_attn_abi_version(void) { return 6; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -312,6 +314,42 @@ int hlm_ce_rows(void* logits, int logits_dtype, int64_t row_stride, const int64_
                                              static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "cross-entropy launch failed: %s", hipGetErrorString(err));
   return HLM_ATTN_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int run_residual_rms_norm(bool backward, const void* a, const void* b, const void* c, void* y0, void* y1,
+                          int64_t rows, int n, float eps, void* stream) {
+  g_last_error[0] = '\0';
+  if (rows < 0 || n <= 0) return fail(HLM_ATTN_EINVAL, "bad shape rows=%lld n=%d", (long long)rows, n);
+  if (n % 8 != 0 || n > 8192)
+    return fail(HLM_ATTN_EUNSUPPORTED, "row width %d must be a multiple of 8 and at most 8192", n);
+  if (!(eps > 0.f) || !std::isfinite(eps)) return fail(HLM_ATTN_EINVAL, "eps must be positive and finite");
+  if ((rows + 3) / 4 >= ((int64_t)1 << 31)) return fail(HLM_ATTN_EUNSUPPORTED, "too many rows for one launch");
+  if (rows == 0) return HLM_ATTN_OK;
+  const void* ptrs[5] = {a, b, backward ? c : a, y0, backward ? y0 : y1};
+  for (const void* q : ptrs)
+    if (q == nullptr || !aligned16(q)) return fail(HLM_ATTN_EINVAL, "a tensor is null or not 16-byte aligned");
+  const hipError_t err =
+      hlm::launch_residual_rms_norm(a, b, c, y0, y1, rows, n, eps, backward, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "residual_rms_norm launch failed: %s", hipGetErrorString(err));
+  return HLM_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hlm_residual_rms_norm_fwd(const void* residual, const void* branch, void* out, void* normed, int64_t rows, int n,
+                              float eps, void* stream) {
+  return run_residual_rms_norm(false, residual, branch, nullptr, out, normed, rows, n, eps, stream);
+}
+
+int hlm_residual_rms_norm_bwd(const void* out, const void* grad_out, const void* grad_normed, void* grad_in,
+                              int64_t rows, int n, float eps, void* stream) {
+  return run_residual_rms_norm(true, out, grad_out, grad_normed, grad_in, nullptr, rows, n, eps, stream);
 }
 
 }  // extern "C"

@@ -238,3 +238,19 @@ def fused_linear_cross_entropy_with_weight(
     if hidden_flat.device.type != "cuda":
         raise RuntimeError("the hip fused linear cross entropy runs on ROCm devices only")
     return _HipFusedLinearCrossEntropy.apply(hidden_flat, weight, targets_flat, bias, chunk_size)
+
+
+# --- residual add + RMSNorm (OutputProjection / DownProjection) --------------------
+
+
+def residual_rms_norm_hip(residual: torch.Tensor, branch: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """residual_rms_norm (model.py:73-75) on the GPU: (out, normed), bf16,
+    out = residual + branch and normed = RMSNorm(out) without weight.
+    Differentiable in residual and branch.  No CPU path."""
+    from . import ops
+
+    if residual.device.type != "cuda":
+        raise RuntimeError("residual_rms_norm_hip runs on ROCm devices only; use the torch path on the CPU")
+    if ops.direct_call_ok(residual, branch):  # inference: same kernel, without the dispatcher's host cost
+        return ops.residual_rms_norm_impl(residual, branch, float(eps))
+    return ops.hip_residual_rms_norm(residual, branch, float(eps))

@@ -1,5 +1,6 @@
-"""AttentionCore, QKVProjection and LMHeadProjection with the hip backend,
-mirroring hackable-lm's model.py:129-250, model.py:50-126 and model.py:317-352.
+"""AttentionCore, QKVProjection, OutputProjection, DownProjection and
+LMHeadProjection with the hip backend, mirroring hackable-lm's
+model.py:129-250, :50-126, :253-264, :295-304 and :317-352.
 
 The reference picks `fwd_<attention_backend>` per call (model.py:169-174);
 this class carries the same per-layer window (model.py:136), the same
@@ -53,6 +54,10 @@ class AttentionConfig:
     vocab_size: int = 0
     loss_chunk_size: int | None = 4096
     lm_head_backend: str = "hip"
+    # OutputProjection / DownProjection fields (config.py:213-232)
+    mlp_hidden: int = 0
+    output_backend: str = "hip"
+    down_backend: str = "hip"
 
 
 class RotaryEmbedding(nn.Module):
@@ -179,3 +184,49 @@ class LMHeadProjection(nn.Module):
             hidden, self.lm_head.weight, self.lm_head.bias, targets, backend="hip", chunk_size=self.chunk_size
         )
         return None, loss
+
+
+class _ResidualNormProjection(nn.Module):
+    """A projection followed by residual_rms_norm, dispatched on a module
+    backend field like the reference's AcceleratedModule (model.py:19-38)."""
+
+    backend_field = ""
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        backend = normalize_module_backend(self.backend_field, getattr(self.config, self.backend_field))
+        fwd_backend = getattr(self, f"fwd_{backend}", None)
+        if fwd_backend is None:
+            raise RuntimeError(f"{type(self).__name__} does not support backend {backend!r}")
+        return fwd_backend(x, residual)
+
+
+class OutputProjection(_ResidualNormProjection):
+    """model.py:253-264 with the hip residual add + RMSNorm."""
+
+    backend_field = "output_backend"
+
+    def __init__(self, config: AttentionConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.norm_eps = config.norm_eps
+        self.o_proj = nn.Linear(config.n_head * config.head_dim, config.n_embd, bias=False)
+
+    def fwd_hip(self, y: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        bsz, seq_len, n_head, head_dim = y.shape
+        y = y.reshape(bsz, seq_len, n_head * head_dim)
+        return kernels.residual_rms_norm_hip(residual, self.o_proj(y), self.norm_eps)
+
+
+class DownProjection(_ResidualNormProjection):
+    """model.py:295-304 with the hip residual add + RMSNorm."""
+
+    backend_field = "down_backend"
+
+    def __init__(self, config: AttentionConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.norm_eps = config.norm_eps
+        self.down_proj = nn.Linear(config.mlp_hidden, config.n_embd, bias=False)
+
+    def fwd_hip(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        return kernels.residual_rms_norm_hip(residual, self.down_proj(x), self.norm_eps)

@@ -380,3 +380,92 @@ def hip_linear_ce(logits: torch.Tensor, targets: torch.Tensor, n_tokens: int) ->
 @hip_linear_ce.register_fake
 def _(logits, targets, n_tokens):
     return logits.new_empty((logits.shape[0],), dtype=torch.float32)
+
+
+# --- residual add + RMSNorm after the output / down projections -------------------
+#
+# hackable_lm::hip_residual_rms_norm computes residual_rms_norm
+# (/root/reference/model.py:73-75) on the GPU; the reference leaves its
+# backward to autograd, here it is hackable_lm::hip_residual_rms_norm_backward.
+
+
+def _rows_ready(t: torch.Tensor, n: int) -> torch.Tensor:
+    """t as a contiguous, 16-byte aligned bf16 (rows, n) tensor."""
+    t = t.to(_BF16).reshape(-1, n)
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.contiguous() if not t.is_contiguous() else t.clone()
+    return t
+
+
+def residual_rms_norm_impl(residual: torch.Tensor, branch: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The launch behind hackable_lm::hip_residual_rms_norm: (out, normed)."""
+    if residual.device.type != "cuda":
+        raise RuntimeError(f"hip residual_rms_norm runs on ROCm devices only, got a tensor on {residual.device}")
+    if residual.shape != branch.shape:
+        raise RuntimeError(f"residual {tuple(residual.shape)} and branch {tuple(branch.shape)} differ")
+    lib = _lib.load()
+    n = residual.shape[-1]
+    a, b = _rows_ready(residual, n), _rows_ready(branch, n)
+    out = torch.empty(residual.shape, dtype=_BF16, device=residual.device)
+    normed = torch.empty(residual.shape, dtype=_BF16, device=residual.device)
+    with _on_device(residual.device):
+        rc = lib.hlm_residual_rms_norm_fwd(
+            a.data_ptr(), b.data_ptr(), out.data_ptr(), normed.data_ptr(), a.shape[0], n, float(eps),
+            _stream_handle(residual.device),
+        )
+    _lib.check(rc, lib)
+    return out, normed
+
+
+@torch.library.custom_op("hackable_lm::hip_residual_rms_norm", mutates_args=())
+def hip_residual_rms_norm(residual: torch.Tensor, branch: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    return residual_rms_norm_impl(residual, branch, eps)
+
+
+@hip_residual_rms_norm.register_fake
+def _(residual, branch, eps):
+    return residual.new_empty(residual.shape, dtype=_BF16), residual.new_empty(residual.shape, dtype=_BF16)
+
+
+@torch.library.custom_op("hackable_lm::hip_residual_rms_norm_backward", mutates_args=())
+def hip_residual_rms_norm_backward(
+    out: torch.Tensor, grad_out: torch.Tensor, grad_normed: torch.Tensor, eps: float
+) -> torch.Tensor:
+    if out.device.type != "cuda":
+        raise RuntimeError(f"hip residual_rms_norm runs on ROCm devices only, got a tensor on {out.device}")
+    lib = _lib.load()
+    n = out.shape[-1]
+    o, go, gn = _rows_ready(out, n), _rows_ready(grad_out, n), _rows_ready(grad_normed, n)
+    grad_in = torch.empty(out.shape, dtype=_BF16, device=out.device)
+    with _on_device(out.device):
+        rc = lib.hlm_residual_rms_norm_bwd(
+            o.data_ptr(), go.data_ptr(), gn.data_ptr(), grad_in.data_ptr(), o.shape[0], n, float(eps),
+            _stream_handle(out.device),
+        )
+    _lib.check(rc, lib)
+    return grad_in
+
+
+@hip_residual_rms_norm_backward.register_fake
+def _(out, grad_out, grad_normed, eps):
+    return out.new_empty(out.shape, dtype=_BF16)
+
+
+def _res_setup_context(ctx, inputs, output):
+    _, _, eps = inputs
+    out, _ = output
+    ctx.save_for_backward(out)
+    ctx.eps = eps
+
+
+def _res_backward(ctx, grad_out, grad_normed):
+    (out,) = ctx.saved_tensors
+    if grad_out is None:
+        grad_out = torch.zeros_like(out)
+    if grad_normed is None:
+        grad_normed = torch.zeros_like(out)
+    g = hip_residual_rms_norm_backward(out, grad_out, grad_normed, ctx.eps)
+    return g, g, None
+
+
+hip_residual_rms_norm.register_autograd(_res_backward, setup_context=_res_setup_context)

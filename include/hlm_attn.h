@@ -197,6 +197,28 @@ int hlm_qk_norm_rope_bwd(const void* q, const void* k, const void* grad_q_out, c
 int hlm_ce_rows(void* logits, int logits_dtype, int64_t row_stride, const int64_t* targets, float* loss, int n_rows,
                 int n_cols, int64_t n_tokens, int ignore_index, void* stream);
 
+/*
+ * Residual add + RMSNorm (no weight) after an output or down projection:
+ * for rows of n bf16 values (contiguous, 16-byte aligned, n a multiple of 8,
+ * n <= 8192)
+ *   out    = residual + branch                  (bf16, as the bf16 add rounds it)
+ *   normed = out * rsqrt(mean(out^2) + eps)     (fp32 from the rounded out, bf16)
+ * Replaces residual_rms_norm (/root/reference/model.py:73-75) in
+ * OutputProjection.fwd_torch (/root/reference/model.py:261-264) and
+ * DownProjection.fwd_torch (/root/reference/model.py:303-304).
+ */
+int hlm_residual_rms_norm_fwd(const void* residual, const void* branch, void* out, void* normed, int64_t rows, int n,
+                              float eps, void* stream);
+
+/*
+ * Its backward: grad_in = grad_out + r (grad_normed - z mean(grad_normed z)),
+ * r = rsqrt(mean(out^2) + eps), z = out r, from the forward's `out`; grad_in
+ * is the gradient of both residual and branch.  Same layout rules.  (The
+ * reference leaves this to autograd.)
+ */
+int hlm_residual_rms_norm_bwd(const void* out, const void* grad_out, const void* grad_normed, void* grad_in,
+                              int64_t rows, int n, float eps, void* stream);
+
 /* Message describing the last failed call on this thread ("" if none). */
 const char* hlm_attn_last_error(void);
 

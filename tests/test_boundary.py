@@ -26,7 +26,7 @@ HEADER = REPO / "include" / "hlm_attn.h"
 
 def declared_symbols() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(hlm_(?:attn|qk|ce)_\w+)\s*\(", text))
+    return set(re.findall(r"\b(hlm_(?:attn|qk|ce|residual)_\w+)\s*\(", text))
 
 
 # --- the shared library -------------------------------------------------------
@@ -462,3 +462,41 @@ def test_fused_linear_ce_refuses_cpu_tensors_and_other_backends():
     cfg = model.AttentionConfig(n_layer=1, n_head=1, n_kv_head=1, n_embd=8, vocab_size=5, lm_head_backend="torch")
     with pytest.raises(RuntimeError, match="does not support backend"):
         model.LMHeadProjection(cfg)(h[None], t[None])
+
+
+# --- residual add + RMSNorm -------------------------------------------------------
+
+def test_residual_rms_norm_validates_before_touching_the_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    fwd = lib.hlm_residual_rms_norm_fwd
+    bwd = lib.hlm_residual_rms_norm_bwd
+    for n, code in ((12, -2), (8200, -2), (0, -1)):
+        assert fwd(p, p, p, p, 4, n, 1e-6, None) == code
+    assert fwd(p, p, p, p, 4, 64, 0.0, None) == -1 and b"eps" in lib.hlm_attn_last_error()
+    assert fwd(p, ctypes.c_void_p(0x1008), p, p, 4, 64, 1e-6, None) == -1
+    assert bwd(p, p, None, p, 4, 64, 1e-6, None) == -1
+    assert fwd(p, p, p, p, 0, 64, 1e-6, None) == 0 and bwd(None, None, None, None, 0, 64, 1e-6, None) == 0
+
+
+def test_residual_rms_norm_refuses_cpu_and_dispatches_on_backend_fields():
+    x = torch.randn(1, 4, 64)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        hlm_attn.residual_rms_norm_hip(x, x, 1e-6)
+    cfg = model.AttentionConfig(n_layer=1, n_head=1, n_kv_head=1, n_embd=64, head_dim=64, mlp_hidden=128,
+                                output_backend="torch", down_backend="triton")
+    with pytest.raises(RuntimeError, match="does not support backend"):
+        model.OutputProjection(cfg)(torch.randn(1, 4, 1, 64), x)
+    with pytest.raises(RuntimeError, match="does not support backend"):
+        model.DownProjection(cfg)(torch.randn(1, 4, 128), x)
+    with FakeTensorModeCtx():
+        r = torch.empty(2, 5, 64, dtype=torch.bfloat16)
+        out, normed = ops.hip_residual_rms_norm(r, r, 1e-6)
+        assert out.shape == r.shape and normed.dtype == torch.bfloat16
+        assert ops.hip_residual_rms_norm_backward(r, r, r, 1e-6).shape == r.shape
+
+
+def FakeTensorModeCtx():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    return FakeTensorMode()
