@@ -67,7 +67,15 @@ def attention(
 ) -> torch.Tensor:
     """Causal (sliding-window) attention on (B, T, H, D) tensors through the HIP
     kernels.  window_size=None is plain causal; window_size=W lets query i see
-    keys i-W+1..i.  Differentiable in q, k and v."""
+    keys i-W+1..i.  Differentiable in q, k and v.
+
+    The kernels take head dims 64 and 128 with Dv = Dqk.  Other head dims up
+    to 128, and Dv != Dqk (model.py:181-184 allows it; the reference test
+    uses Dqk = 7, Dv = 9, tests/test_kernels.py:103-105), run on them with
+    the head dims zero-padded to the next of 64 / 128: zero columns of q and
+    k leave q.k unchanged, zero columns of v only add zero output columns
+    (sliced off), and the scale stays 1/sqrt(Dqk).  Gradients flow back
+    through the padding exactly."""
     from . import ops  # registers the custom ops on first use
 
     if q.dtype != torch.bfloat16:
@@ -81,11 +89,27 @@ def attention(
     if window_size is not None and window_size < 1:
         raise RuntimeError(f"window_size must be >= 1 or None, got {window_size}")
     window = 0 if window_size is None else int(window_size)
+    dqk, dv = q.shape[-1], v.shape[-1]
+    if k.shape[-1] != dqk:
+        raise RuntimeError(f"q head dim {dqk} and k head dim {k.shape[-1]} differ")
+    d_kernel = padded_head_dim(dqk, dv)
+    if d_kernel != dqk or d_kernel != dv:
+        pad = torch.nn.functional.pad
+        q, k = pad(q, (0, d_kernel - dqk)), pad(k, (0, d_kernel - dqk))
+        v = pad(v, (0, d_kernel - dv))
     if ops.direct_call_ok(q, k, v):  # inference: same kernels, without the dispatcher's host cost
         out, _ = ops.attn_fwd_impl(q, k, v, window, float(scale))
-        return out
-    out, _ = ops.hip_attn_fwd(q, k, v, window, float(scale))
-    return out
+    else:
+        out, _ = ops.hip_attn_fwd(q, k, v, window, float(scale))
+    return out if d_kernel == dv else out[..., :dv]
+
+
+def padded_head_dim(dqk: int, dv: int) -> int:
+    """The kernel head dim that (Dqk, Dv) run at: 64 or 128."""
+    d = max(dqk, dv)
+    if d < 1 or d > 128:
+        raise RuntimeError(f"head dims ({dqk}, {dv}) are not supported: the kernels take at most 128")
+    return 64 if d <= 64 else 128
 
 
 def scaled_dot_product_attention(

@@ -500,3 +500,25 @@ def FakeTensorModeCtx():
     from torch._subclasses.fake_tensor import FakeTensorMode
 
     return FakeTensorMode()
+
+
+def test_other_head_dims_run_zero_padded(fake_op):
+    """Dv != Dqk (the reference test's Dqk = 7, Dv = 9, tests/test_kernels.py:103-105)
+    and head dims other than 64 / 128 reach the kernels zero-padded to 64 or
+    128, with the scale of the true Dqk and the output sliced back to Dv."""
+    q = torch.randn(1, 5, 2, 7)
+    v = torch.randn(1, 5, 2, 9)
+    out = kernels.attention(q, q, v)
+    _, _, _, qs, ks, _, scale = fake_op.calls[-1]
+    assert qs[-1] == 64 and ks[-1] == 64 and math.isclose(scale, 7 ** -0.5)
+    assert out.shape == (1, 5, 2, 9)
+    # the fake op echoes q, so the output columns are q's: padding kept q's
+    # first 7 columns, zeros after
+    assert torch.equal(out[..., :7], q.bfloat16()) and torch.count_nonzero(out[..., 7:]) == 0
+    kernels.attention(torch.randn(1, 5, 2, 96), torch.randn(1, 5, 2, 96), torch.randn(1, 5, 2, 80))
+    assert fake_op.calls[-1][3][-1] == 128
+    assert kernels.padded_head_dim(64, 64) == 64 and kernels.padded_head_dim(65, 8) == 128
+    with pytest.raises(RuntimeError, match="at most 128"):
+        kernels.attention(torch.randn(1, 5, 2, 192), torch.randn(1, 5, 2, 192), torch.randn(1, 5, 2, 192))
+    with pytest.raises(RuntimeError, match="differ"):
+        kernels.attention(torch.randn(1, 5, 2, 64), torch.randn(1, 5, 2, 32), torch.randn(1, 5, 2, 64))
