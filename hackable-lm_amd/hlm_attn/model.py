@@ -7,7 +7,7 @@ this class carries the same per-layer window (model.py:136), the same
 window-or-None rule at call time (model.py:155-159) and the same
 (B, T, H, D) in / (B, T, H, D) out layout as `fwd_flash_attn_2`
 (model.py:216-226).  `fwd_hip` is the method the reference's AttentionCore
-gains when the backend is registered there.
+gains when the backend is registered there, next to `fwd_flash_attn_2`.
 
 QKVProjection mirrors model.py:76-126: the fused q/k/v projection, then the
 q/k RMSNorm + partial RoPE producer; `fwd_hip` is `fwd_triton` with the HIP
