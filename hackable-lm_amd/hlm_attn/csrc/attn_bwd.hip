@@ -524,13 +524,42 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   const int wk_hi = min(kw0 + 31, T - 1);
   int cp_t = 0;  // query tile (within the current head) of the compute pointer
 
-  for (int it = 0; it < n_iter; ++it) {
+  // The tile loop is unrolled by the ring depth, so each copy of the body
+  // reads a fixed slot: its LDS addresses are a per-lane register (slot 0's
+  // address, lane part included, made opaque so it is not re-associated)
+  // plus a constant that the ds_read offset field carries.  No address
+  // arithmetic is left in the loop (24 VALU instructions per tile fewer at
+  // D = 64).  D = 128 has no registers to spare for them and recomputes
+  // the lane part, still with the slot constant folded.
+  static_assert(NBUF % 2 == 0, "a slot's parity is its tile's parity");
+  unsigned ab_s[NS] = {}, atr[NDB][2] = {};
+  if constexpr (KEEP_TRO) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      ab_s[s] = lring + (unsigned)off_s[s];
+      asm volatile("" : "+v"(ab_s[s]));
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        atr[db][k] = lring + (unsigned)tro[db][k];
+        asm volatile("" : "+v"(atr[db][k]));
+      }
+  }
+  const unsigned lbase = KEEP_TRO ? 0u : lring;  // the part of the ring address not in ab_s / atr
+
+  for (int it0 = 0; it0 < n_iter; it0 += NBUF)
+#pragma unroll
+  for (int slot = 0; slot < NBUF; ++slot) {
+    const int it = it0 + slot;
+    if (it >= n_iter) break;
     // Every second tile: wait for this wave's copies of tiles it and it + 1
     // (newer tiles may stay in flight); the barrier makes every wave's copies
     // visible and frees the slots of tiles it - 2 and it - 1 (and, at it = 0,
     // the staging area); then the ring is topped up to NBUF - 1 tiles past
     // it.  Tile it + 1 then needs no barrier of its own.
-    if ((it & 1) == 0) {
+    if ((slot & 1) == 0) {
       const int need = min(it + 1, n_iter - 1);
       if (wave < 2)
         dma_barrier_upto<PER + 1, NBUF - 1>(issued - 1 - need);
@@ -540,8 +569,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
       while (issued < want) load_tile();
     }
 
-    const int slot = it % NBUF;
-    const unsigned qs_t = lring + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
+    const unsigned qs_t = lbase + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
     const float* st = stbuf[slot];
     const int qs = (tq_lo + cp_t) * BMQ;
     if (++cp_t == nq) cp_t = 0;
@@ -575,7 +603,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     f32x16 sacc = si, pacc = di;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int o = offs(s);
+      const int o = KEEP_TRO ? (int)ab_s[s] : offs(s);
       sacc = mfma32(cs_operand<D>(qs_t, o, 0), kreg[s], sacc);
       pacc = mfma32(cs_operand<D>(ds_t, o, 0), vreg[s], pacc);
     }
@@ -590,8 +618,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const int o0 = KEEP_TRO ? tro[db][0] : cs_tr_off<D>(db, 0, lane);
-        const int o1 = KEEP_TRO ? tro[db][1] : cs_tr_off<D>(db, 1, lane);
+        const int o0 = KEEP_TRO ? (int)atr[db][0] : cs_tr_off<D>(db, 0, lane);
+        const int o1 = KEEP_TRO ? (int)atr[db][1] : cs_tr_off<D>(db, 1, lane);
         dvacc[db] = mfma32(cs_operand_tr<D>(ds_t, o0, o1, 16 * kk), pb[kk], dvacc[db]);
         dkacc[db] = mfma32(cs_operand_tr<D>(qs_t, o0, o1, 16 * kk), dsb[kk], dkacc[db]);
       }

@@ -152,8 +152,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   const int wq_hi = min(qw0 + 31, T - 1);
   const float c = a.scale_log2;
 
+  // The tile loop is unrolled by the ring depth, so each copy of the body
+  // reads a fixed slot: its LDS addresses are a per-lane register (slot 0's
+  // address, lane part included, opaque so that it is not re-associated) plus
+  // a constant carried by the ds_read offset field -- no address arithmetic
+  // in the loop.
+  unsigned ab_s[NS], atr[NDB][2];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    ab_s[s] = lring + (unsigned)off_s[s];
+    asm volatile("" : "+v"(ab_s[s]));
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      atr[db][k] = lring + (unsigned)tro[db][k];
+      asm volatile("" : "+v"(atr[db][k]));
+    }
+
   int issued_hi = n_pre - 1;
-  for (int it = 0; it < n_tiles; ++it) {
+  for (int it0 = 0; it0 < n_tiles; it0 += NBUF)
+#pragma unroll
+  for (int slot = 0; slot < NBUF; ++slot) {
+    const int it = it0 + slot;
+    if (it >= n_tiles) break;
     // Wait for this wave's copies of tile it (newer tiles may stay in flight);
     // the barrier makes every wave's copies visible and frees the slot of tile
     // it - 1 (and, at it = 0, the staging area); then the ring is topped up to
@@ -162,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     const int want = min(it + NBUF - 1, n_tiles - 1);
     while (issued_hi < want) load_tile(++issued_hi);
 
-    const unsigned kt = lring + (unsigned)(it % NBUF) * SLOTB, vt = kt + TILEB;
+    const unsigned kt = (unsigned)slot * SLOTB, vt = kt + TILEB;  // constants; lring is in ab_s / atr
     const int k0 = (t_lo + it) * BN;
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
@@ -172,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     for (int kb = 0; kb < BN / 32; ++kb) {
       sacc[kb] = zero16();
 #pragma unroll
-      for (int s = 0; s < NS; ++s) sacc[kb] = mfma32(cs_operand<D>(kt, off_s[s], kb), qreg[s], sacc[kb]);
+      for (int s = 0; s < NS; ++s) sacc[kb] = mfma32(cs_operand<D>(kt, (int)ab_s[s], kb), qreg[s], sacc[kb]);
     }
     if (!full) {
       // key = k0 + 4 h32 + (32 kb + 8 i + j) is visible iff 0 <= myq - key < W.
@@ -229,7 +252,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int kk = 0; kk < BN / 16; ++kk)
-        oacc[db] = mfma32(cs_operand_tr<D>(vt, tro[db][0], tro[db][1], 16 * kk), pb[kk], oacc[db]);
+        oacc[db] = mfma32(cs_operand_tr<D>(vt, (int)atr[db][0], (int)atr[db][1], 16 * kk), pb[kk], oacc[db]);
   }
 
   if constexpr (SPLIT) {
