@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   static_assert(PRE >= 1, "the loop waits for tile 0 at its first barrier");
   static_assert(PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
   static_assert(NBUF * PER < 64 && 2 * NCH + PRE * PER < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
+  __shared__ __attribute__((aligned(2048))) char ring[NBUF * SLOTB];
 
   const int T = a.T, W = a.W, H = a.H;
   const int nqt = (T + BM - 1) / BM;
@@ -211,110 +211,78 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   constexpr int KG = D == 64 ? 2 : 1;
   static_assert(PRE >= KG && NBUF >= 2 * KG + 1, "the first group is in flight before the loop");
   if constexpr (D == 64) {
+    // Unrolled by the ring depth like the D = 128 loop below: fixed slots per
+    // copy, ring base folded into two per-lane registers.  Their XOR variants
+    // (valid with the base included: the ring is 2 KB aligned and the XORed
+    // bits 5, 6 and 10 lie below that, as do the offsets they act on) are
+    // formed per tile from copies made opaque in each iteration, so they are
+    // not hoisted into registers of their own.
+    static_assert(NBUF % KG == 0, "a group never straddles two passes of the unrolled loop");
+    const unsigned ab0 = lring + (unsigned)off_s[0], at00 = lring + (unsigned)tro[0][0];
     int issued_hi = n_pre - 1;
-    unsigned kt = lring;  // ring slot of tile it
-    for (int it = 0; it < n_tiles; ++it) {
-      // At the first tile of each group: wait for this wave's copies of the
-      // group (newer tiles may stay in flight); the barrier makes every wave's
-      // copies visible and frees the slots of the previous group (and, at it =
-      // 0, the staging area); then the ring is topped up to NBUF - 1 tiles past
-      // it.  In the steady state (KG <= it <= n_tiles - NBUF) exactly NBUF - 2 KG
-      // tiles are in flight behind the group and KG tiles are copied, into the
-      // slots just freed: no counting branches.
-      if (it % KG == 0) {
+    for (int it0 = 0; it0 < n_tiles; it0 += NBUF)
+#pragma unroll
+    for (int slot = 0; slot < NBUF; ++slot) {
+      const int it = it0 + slot;
+      if (it >= n_tiles) break;
+      if (slot % KG == 0) {
         if (it >= KG && it + NBUF - 1 <= n_tiles - 1) {
           dma_barrier<(NBUF - 2 * KG) * PER>();
-          unsigned ks = kt;
-  #pragma unroll
-          for (int m = 0; m < KG; ++m) ks = ks == lring ? lring + (NBUF - 1) * SLOTB : ks - SLOTB;
-  #pragma unroll
-          for (int m = 0; m < KG; ++m) {  // slots of tiles it - KG .. it - 1
-            load_tile_at(++issued_hi, ks);
-            ks = ks == lring + (NBUF - 1) * SLOTB ? lring : ks + SLOTB;
-          }
+#pragma unroll
+          for (int m = 0; m < KG; ++m)  // slots of tiles it - KG .. it - 1
+            load_tile_at(++issued_hi, lring + (unsigned)((slot - KG + m + NBUF) % NBUF) * SLOTB);
         } else {
           dma_barrier_upto<PER, NBUF - 1>(issued_hi - min(it + KG - 1, n_tiles - 1));
           const int want = min(it + NBUF - 1, n_tiles - 1);
           while (issued_hi < want) load_tile(++issued_hi);
         }
       }
-      const unsigned vt = kt + TILEB;
-      const unsigned knext = kt == lring + (NBUF - 1) * SLOTB ? lring : kt + SLOTB;
+      const unsigned kt = (unsigned)slot * SLOTB, vt = kt + TILEB;  // constants; the base is in ab / tb
       const int k0 = (t_lo + it) * BN;
-      if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) {
-        kt = knext;
-        continue;
-      }
+      if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
       const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
-      if constexpr (kBatchReads) {
-        // All operand reads of S and dP are issued before the first MFMA.
-        bf16x8 kop[NS], vop[NS];
-        // off_s[s] == off_s[0] ^ 32 s (the swizzle permutes 16-byte units within a
-        // row, and unit 2 s + h32 differs from unit h32 in bits 1.. only).
-        int ob = off_s[0], tb = tro[0][0];
-        asm volatile("" : "+v"(ob), "+v"(tb));
-  #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          kop[s] = cs_operand<D>(kt, ob ^ (32 * s), 0);
-          vop[s] = cs_operand<D>(vt, ob ^ (32 * s), 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        f32x16 sacc;
-        if (full) {
-          sacc = mfma32(kop[0], qreg[0], slse);
-        } else {
-          // Column c = 4 h32 + 8 (x / 4) + x % 4 of the tile is key k0 + c; it is
-          // visible to row myq iff d0 - W < c <= d0 with d0 = myq - k0 - 4 h32.
-          const int d0 = myq - k0 - 4 * h32;
-          const unsigned vis = band_bits(d0 - W + 1, d0);
-          f32x16 st = slse;
-  #pragma unroll
-          for (int x = 0; x < 16; ++x) {
-            const int cst = 8 * (x >> 2) + (x & 3);
-            st[x] = ((vis >> cst) & 1u) ? st[x] : -INFINITY;
-          }
-          sacc = mfma32(kop[0], qreg[0], st);
-        }
-        f32x16 pacc = mfma32(vop[0], doreg[0], sdel);
-  #pragma unroll
-        for (int s = 1; s < NS; ++s) {
-          sacc = mfma32(kop[s], qreg[s], sacc);
-          pacc = mfma32(vop[s], doreg[s], pacc);
-        }
-        bf16x8 dsb[2];
-  #pragma unroll
-        for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
-  #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-  #pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            dqacc[db] = mfma32(cs_operand_tr<D>(kt, cs_tr_off_from<D>(tb, db, 0), cs_tr_off_from<D>(tb, db, 1), 16 * kk), dsb[kk], dqacc[db]);
-      } else {
-        f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
-        if (!full) {
-          // key = k0 + 4 h32 + 8 (x / 4) + x % 4 is visible iff 0 <= myq - key < W.
-          const int d0 = myq - k0 - 4 * h32;
-  #pragma unroll
-          for (int x = 0; x < 16; ++x) {
-            const int cst = 8 * (x >> 2) + (x & 3);
-            sacc[x] = (unsigned)(d0 - cst) < (unsigned)W ? sacc[x] : -INFINITY;
-          }
-        }
-  #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          sacc = mfma32(cs_operand<D>(kt, off_s[s], 0), qreg[s], sacc);
-          pacc = mfma32(cs_operand<D>(vt, off_s[s], 0), doreg[s], pacc);
-        }
-        bf16x8 dsb[2];
-  #pragma unroll
-        for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
-  #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-  #pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            dqacc[db] = mfma32(cs_operand_tr<D>(kt, tro[db][0], tro[db][1], 16 * kk), dsb[kk], dqacc[db]);
+      // All operand reads of S and dP are issued before the first MFMA.
+      bf16x8 kop[NS], vop[NS];
+      unsigned ab = ab0, tb = at00;
+      asm volatile("" : "+v"(ab), "+v"(tb));
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kop[s] = cs_operand<D>(kt, (int)(ab ^ (32u * s)), 0);
+        vop[s] = cs_operand<D>(vt, (int)(ab ^ (32u * s)), 0);
       }
-      kt = knext;
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 sacc;
+      if (full) {
+        sacc = mfma32(kop[0], qreg[0], slse);
+      } else {
+        // Column c = 4 h32 + 8 (x / 4) + x % 4 of the tile is key k0 + c; it is
+        // visible to row myq iff d0 - W < c <= d0 with d0 = myq - k0 - 4 h32.
+        const int d0 = myq - k0 - 4 * h32;
+        const unsigned vis = band_bits(d0 - W + 1, d0);
+        f32x16 st = slse;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          const int cst = 8 * (x >> 2) + (x & 3);
+          st[x] = ((vis >> cst) & 1u) ? st[x] : -INFINITY;
+        }
+        sacc = mfma32(kop[0], qreg[0], st);
+      }
+      f32x16 pacc = mfma32(vop[0], doreg[0], sdel);
+#pragma unroll
+      for (int s = 1; s < NS; ++s) {
+        sacc = mfma32(kop[s], qreg[s], sacc);
+        pacc = mfma32(vop[s], doreg[s], pacc);
+      }
+      bf16x8 dsb[2];
+#pragma unroll
+      for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dqacc[db] = mfma32(cs_operand_tr<D>(kt, cs_tr_off_from<D>((int)tb, db, 0), cs_tr_off_from<D>((int)tb, db, 1),
+                                              16 * kk),
+                             dsb[kk], dqacc[db]);
     }
   } else {
     // D = 128 (one tile per group): the loop unrolled by the ring depth, so
