@@ -7,26 +7,33 @@ workload cfg2: B=8, H=12, T=2048, D=64, window=512, causal, bf16, synthetic
 N(0,1) inputs from one seed, resident in HBM before timing starts.  Warm
 cache: steps run back to back, as in training.
 
-Prints ONE JSON line: value = effective fwd+bwd TFLOP/s, where effective FLOPs
-count only unmasked (query, key) pairs P(T, W): fwd 4*D*P, bwd 8*D*P per
-(batch, head).  Also reports ms per layer (fwd, bwd, fwd+bwd), the fraction of
-MI355X's dense bf16 MFMA peak, a roofline object for the dominant kernel
-(HIP-event timed on the launch stream) and the CPU baseline: the reference's
-`torch` backend restated on the host CPU (configs[0] shape, fp32, forward).
-A "producer" object times the q/k RMSNorm + partial RoPE kernels that feed
-attention (forward and backward) at cfg2's q/k shape against the HBM roofline;
-an "eval" object times the evaluation harness's no-grad forwards at batch 1
-and ragged T; an "lm_head" object times the LM head's cross-entropy rows
-and a "residual_norm" object the residual add + RMSNorm, both against the
-HBM roofline.
+Timing.  A time-based pre-warm runs steps until the GPU has done >= 200 ms of
+work and the last 10 step times agree within 2% (the clock ramps for the first
+~100 steps after idling), independent of --warmup; then --warmup untimed
+steps; then exactly --steps steps between two HIP events on the launch stream
+(torch's current stream, which the C ABI launches on), synchronised before and
+after.  value = effective fwd+bwd TFLOP/s of those steps, where effective
+FLOPs count only unmasked (query, key) pairs P(T, W): fwd 4*D*P, bwd 8*D*P per
+(batch, head).  Wall-clock time of the same steps is a side field.
+
+Prints ONE JSON line with, besides the contract fields: ms per layer (fwd,
+bwd, fwd+bwd), the fraction of MI355X's dense bf16 MFMA peak, per-kernel
+launch times, a roofline object for the dominant kernel (HIP-event mean over
+back-to-back launches), the CPU baseline (the reference's `torch` backend
+restated, configs[0] shape, fp32 forward, on the host's cores), and a
+"configs" object with every other BASELINE GPU config measured in the same
+run: cfg3 (one full-causal layer), cfg4 (the 18-layer stack, per layer and in
+total) and cfg5 (q and k RoPE-rotated before the bf16 cast).  "producer",
+"eval", "lm_head" and "residual_norm" objects time the neighbouring kernels
+(q/k RMSNorm + RoPE, no-grad batch-1 forwards, LM-head cross-entropy rows,
+residual add + RMSNorm) against their rooflines.
 
 Steps are eager launches by default (they run ahead of the GPU); --graph times
 HIP-graph replays of one captured step instead (the way a training step runs
-under torch.compile's CUDA-graph mode).  The default warmup (300 steps) lets
-the GPU reach its steady clock before timing starts.
+under torch.compile's CUDA-graph mode).
 
-  python bench.py [--steps K] [--warmup W] [--config NAME] [--sweep] [--no-cpu-baseline] [--graph]
-                  [--no-producer] [--no-eval] [--no-lm-head]
+  python bench.py [--steps K] [--warmup W] [--config NAME] [--kernel-reps N] [--no-configs] [--cold]
+                  [--no-cpu-baseline] [--graph] [--no-producer] [--no-eval] [--no-lm-head] [--copy-mib M]
 """
 from __future__ import annotations
 
@@ -87,7 +94,10 @@ def algorithmic_bytes(cfg: dict) -> dict:
 class Problem:
     """Device buffers and C-ABI launches for one configuration."""
 
-    def __init__(self, cfg: dict, seed: int, device):
+    def __init__(self, cfg: dict, seed: int, device, tensors=None):
+        """q, k, v, dO ~ N(0,1) from a CPU generator seeded with `seed`,
+        rounded to bf16 and copied to the device; or `tensors` = (q, k, v, dO),
+        bf16 device tensors of this shape prepared by the caller."""
         import torch
         from hlm_attn import _lib
 
@@ -95,9 +105,12 @@ class Problem:
         self.lib = _lib.load()
         self.cfg = cfg
         B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["D"]
-        g = torch.Generator(device="cpu").manual_seed(seed)
-        mk = lambda: torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)  # noqa: E731
-        self.q, self.k, self.v, self.do = mk(), mk(), mk(), mk()
+        if tensors is None:
+            g = torch.Generator(device="cpu").manual_seed(seed)
+            mk = lambda: torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)  # noqa: E731
+            self.q, self.k, self.v, self.do = mk(), mk(), mk(), mk()
+        else:
+            self.q, self.k, self.v, self.do = tensors
         self.o = torch.empty_like(self.q)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
         self.lse = torch.empty(B, H, T, dtype=torch.float32, device=device)
@@ -427,31 +440,72 @@ def event_times_ms(torch, fn, reps: int, before=None) -> list[float]:
     return [a.elapsed_time(b) for a, b in pairs_]
 
 
-FLUSH_MB = 512  # cold-cache policy: this many MB are written between timed launches (the MALL is 256 MB)
+FLUSH_MB = 512  # cold-cache policy (--cold): this many MB are written between timed launches (the MALL is 256 MB)
 
 
-def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> dict:
-    """Times `steps` fwd+bwd steps after `warmup` untimed ones.  By default the
-    steps are eager launches from Python (the launches run ahead of the GPU,
-    so this is GPU time); with graph=True one step (its three kernel launches)
-    is captured once in a HIP graph and replayed per step, as a training step
+def prewarm(torch, step, min_ms: float = 200.0, max_s: float = 2.0, block: int = 10, tol: float = 0.02) -> dict:
+    """Runs blocks of `block` steps, each timed by one pair of HIP events on
+    the launch stream, until the GPU has done at least `min_ms` of work AND
+    the last three blocks agree within `tol` of their median, or `max_s`
+    seconds have passed.  The MI355X runs its first ~100 cfg2 steps after
+    idling ~12% slower while its clock ramps; this loop is independent of
+    --warmup, so the timed steps see the steady state however few warmup
+    steps the caller asks for."""
+    blocks: list[float] = []
+    t_end = time.perf_counter() + max_s
+    while True:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(block):
+            step()
+        b.record()
+        b.synchronize()
+        blocks.append(a.elapsed_time(b))
+        last = blocks[-3:]
+        spread = (max(last) - min(last)) / statistics.median(last) if len(last) == 3 else float("inf")
+        converged = sum(blocks) >= min_ms and spread <= tol
+        if converged or time.perf_counter() > t_end:
+            return {
+                "prewarm_ms": round(sum(blocks), 2),
+                "prewarm_steps": block * len(blocks),
+                "prewarm_converged": converged,
+                "prewarm_last_blocks_spread": round(spread, 4),
+                "prewarm_rule": f">= {min_ms:.0f} ms of GPU work and the last 3 blocks of {block} steps within "
+                f"{100 * tol:.0f}% of their median (cap {max_s:.0f} s)",
+            }
+
+
+def timed_steps(torch, step, steps: int) -> tuple[float, float]:
+    """(event ms per step, wall ms per step) over exactly `steps` steps,
+    bracketed by torch.cuda.synchronize() on both sides; the events are
+    recorded on the launch stream (torch's current stream, which the C ABI
+    launches on)."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(end) / steps, wall
+
+
+def measure(name: str, steps: int, warmup: int, device, graph: bool = False, kernel_reps: int = 500,
+            cold: bool = False) -> dict:
+    """cfg `name`: a time-based pre-warm, `warmup` untimed steps, then exactly
+    `steps` fwd+bwd steps timed with HIP events (value / ms_per_step), and
+    each kernel alone over `kernel_reps` back-to-back launches (kernel_us,
+    the roofline).  Steps are eager launches from Python (they run ahead of
+    the GPU); with graph=True one step (its three kernel launches) is
+    captured once in a HIP graph and replayed per step, as a training step
     under torch.compile's CUDA-graph mode runs it."""
     import torch
 
     cfg = CONFIGS[name]
     prob = Problem(cfg, seed=0, device=device)
-
-    def eager_wall(n):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(n):
-            prob.step()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e3 / n
-
-    for _ in range(warmup):
-        prob.step()
-    eager_ms = eager_wall(steps)
+    warm = prewarm(torch, prob.step)
     run_step = prob.step
     if graph:
         g = torch.cuda.CUDAGraph()
@@ -464,34 +518,28 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
         with torch.cuda.graph(g):
             prob.step()
         run_step = g.replay
-        for _ in range(warmup):
-            run_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(warmup):
         run_step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms, wall_ms = timed_steps(torch, run_step, steps)
 
-    reps = max(steps, 20)
     kern = {
-        "fwd": event_time_ms(torch, prob.fwd, reps),
-        "bwd_dq": event_time_ms(torch, prob.bwd_dq, reps),
-        "bwd_dkdv": event_time_ms(torch, prob.bwd_dkdv, reps),
+        "fwd": event_time_ms(torch, prob.fwd, kernel_reps),
+        "bwd_dq": event_time_ms(torch, prob.bwd_dq, kernel_reps),
+        "bwd_dkdv": event_time_ms(torch, prob.bwd_dkdv, kernel_reps),
     }
-    bwd_ms = event_time_ms(torch, prob.bwd, reps)
-    step_ms = event_time_ms(torch, run_step, reps)
-    # Per-launch medians, warm (back to back) and cold (a 512 MB buffer
-    # written before each launch evicts the last-level cache).
-    flush_buf = torch.empty(FLUSH_MB * (1 << 20) // 4, dtype=torch.float32, device=device)
-    flush = lambda: flush_buf.fill_(1.0)  # noqa: E731
-    med = {}
-    cold = {}
-    for k, fn in (("fwd", prob.fwd), ("bwd_dq", prob.bwd_dq), ("bwd_dkdv", prob.bwd_dkdv), ("bwd", prob.bwd),
-                  ("fwd_bwd", prob.step)):
-        med[k] = statistics.median(event_times_ms(torch, fn, max(reps, 100)))
-        cold[k] = statistics.median(event_times_ms(torch, fn, 50, before=flush))
-    del flush_buf
+    bwd_ms = event_time_ms(torch, prob.bwd, kernel_reps)
+    out_cold = None
+    if cold:
+        # Per-launch medians with a 512 MB buffer written before each launch
+        # (evicts the last-level cache), beside the warm per-launch medians.
+        flush_buf = torch.empty(FLUSH_MB * (1 << 20) // 4, dtype=torch.float32, device=device)
+        flush = lambda: flush_buf.fill_(1.0)  # noqa: E731
+        out_cold = {"warm_median_us": {}, "cold_median_us": {}}
+        for k, fn in (("fwd", prob.fwd), ("bwd_dq", prob.bwd_dq), ("bwd_dkdv", prob.bwd_dkdv), ("bwd", prob.bwd),
+                      ("fwd_bwd", prob.step)):
+            out_cold["warm_median_us"][k] = round(statistics.median(event_times_ms(torch, fn, 100)) * 1e3, 2)
+            out_cold["cold_median_us"][k] = round(statistics.median(event_times_ms(torch, fn, 50, before=flush)) * 1e3, 2)
+        del flush_buf
     fl = effective_flops(cfg)
     by = algorithmic_bytes(cfg)
     total = fl["fwd"] + fl["bwd"]
@@ -500,21 +548,21 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
     achieved = fl[dominant] / (kern[dominant] * 1e-3) / 1e12
     return {
         "cfg": cfg,
+        "step_ms": step_ms,
         "wall_ms_per_step": wall_ms,
-        "event_ms_per_step": step_ms,
-        "eager_wall_ms_per_step": eager_ms,
+        "prewarm": warm,
         "graph": graph,
         "fwd_ms": kern["fwd"],
         "bwd_ms": bwd_ms,
         "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
-        "median_us": {k: round(v * 1e3, 2) for k, v in med.items()},
-        "cold_us": {k: round(v * 1e3, 2) for k, v in cold.items()},
+        "kernel_reps": kernel_reps,
+        "cold": out_cold,
         "tflops": {
             "fwd": fl["fwd"] / (kern["fwd"] * 1e-3) / 1e12,
             "bwd": fl["bwd"] / (bwd_ms * 1e-3) / 1e12,
-            "fwd_bwd": total / (wall_ms * 1e-3) / 1e12,
+            "fwd_bwd": total / (step_ms * 1e-3) / 1e12,
             # FlashAttention convention: bwd counted as 2.5x fwd (includes the recompute).
-            "fwd_bwd_fa_convention": 3.5 * fl["fwd"] / (wall_ms * 1e-3) / 1e12,
+            "fwd_bwd_fa_convention": 3.5 * fl["fwd"] / (step_ms * 1e-3) / 1e12,
         },
         "dominant": dominant,
         "roofline": {
@@ -524,10 +572,11 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": read_traffic(name, kernel_name),
             "algorithmic_flops_per_launch": fl[dominant],
             "algorithmic_bytes_per_launch": by[dominant],
             "launch_us": round(kern[dominant] * 1e3, 2),
-            "traffic": read_traffic(name, kernel_name),
+            "launches_averaged": kernel_reps,
             # The same launch against the HBM roofline (algorithmic bytes / launch time).
             "hbm": {
                 "achieved_GBs": round(by[dominant] / (kern[dominant] * 1e-3) / 1e9, 1),
@@ -535,6 +584,175 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False) -> 
                 "frac": round(by[dominant] / (kern[dominant] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             },
         },
+    }
+
+
+# ---------------------------------------------------------------------------
+# The other BASELINE configs, measured in the same run ("configs" object).
+# ---------------------------------------------------------------------------
+
+CFG4_LAYERS = dict(n_layer=18, window=1024, full_every=4)
+ROPE_BASE = 10000.0  # RoPE base 10000 over positions 0..T-1, whole head
+
+
+def rope_rotate(x, base: float = ROPE_BASE):
+    """Rotate-half RoPE over the whole head dim (model.py:105-114 with
+    fraction 1.0, theta = base) of a (B, T, H, D) fp32 tensor, positions
+    0..T-1, computed in fp32: the input synthesis of BASELINE configs[4]."""
+    import torch
+
+    T, D = x.shape[1], x.shape[3]
+    inv_freq = 1.0 / (base ** (torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D))
+    freqs = torch.outer(torch.arange(T, device=x.device, dtype=torch.float32), inv_freq)
+    cos, sin = freqs.cos()[None, :, None, :], freqs.sin()[None, :, None, :]
+    x1, x2 = x[..., : D // 2], x[..., D // 2 :]
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1)
+
+
+def device_inputs(cfg: dict, seed: int, device, rope: bool = False):
+    """q, k, v, dO ~ N(0,1) drawn in that order from a device generator seeded
+    with `seed` (fp32, then rounded to bf16); with rope=True, q and k are
+    rotated (rope_rotate) in fp32 before the rounding."""
+    import torch
+
+    B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["D"]
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = []
+    for i in range(4):
+        x = torch.randn(B, T, H, D, generator=g, device=device, dtype=torch.float32)
+        if rope and i < 2:
+            x = rope_rotate(x)
+        out.append(x.to(torch.bfloat16))
+        del x
+    return out
+
+
+def _layer_entry(cfg: dict, fwd_ms: float, bwd_ms: float, step_ms: float) -> dict:
+    fl = effective_flops(cfg)
+    tot = fl["fwd"] + fl["bwd"]
+    return {
+        "ms_per_layer": {"fwd": round(fwd_ms, 5), "bwd": round(bwd_ms, 5), "fwd_bwd": round(step_ms, 5)},
+        "tflops": {
+            "fwd": round(fl["fwd"] / (fwd_ms * 1e-3) / 1e12, 2),
+            "bwd": round(fl["bwd"] / (bwd_ms * 1e-3) / 1e12, 2),
+            "fwd_bwd": round(tot / (step_ms * 1e-3) / 1e12, 2),
+        },
+        "pct_of_bf16_peak": round(100 * tot / (step_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "effective_gflop_fwd_bwd": round(tot / 1e9, 3),
+    }
+
+
+def measure_single_layer(name: str, reps: int, device, rope: bool = False, prewarm_ms: float = 20.0) -> dict:
+    """One layer of config `name`: fwd alone, bwd alone and fwd+bwd steps,
+    each the HIP-event mean over `reps` back-to-back launches, after a short
+    pre-warm (the GPU is already at its steady clock from the headline
+    measurement just before)."""
+    import torch
+
+    cfg = CONFIGS[name]
+    prob = Problem(cfg, seed=0, device=device, tensors=device_inputs(cfg, 0, device, rope=rope))
+    warm = prewarm(torch, prob.step, min_ms=prewarm_ms)
+    step_ms = event_time_ms(torch, prob.step, reps)
+    fwd_ms = event_time_ms(torch, prob.fwd, reps)
+    bwd_ms = event_time_ms(torch, prob.bwd, reps)
+    w = "causal" if cfg["W"] is None else f"window={cfg['W']}"
+    entry = {
+        "workload": f"B={cfg['B']} H={cfg['H']} T={cfg['T']} D={cfg['D']} {w}; q, k, v, dO ~ N(0,1) seed 0"
+        + (f", q and k RoPE-rotated (base {ROPE_BASE:g}, positions 0..T-1, whole head) in fp32 before the bf16 cast"
+           if rope else ""),
+        "reps": reps,
+        "prewarm_ms": warm["prewarm_ms"],
+        "prewarm_converged": warm["prewarm_converged"],
+    }
+    entry.update(_layer_entry(cfg, fwd_ms, bwd_ms, step_ms))
+    del prob
+    torch.cuda.empty_cache()
+    return entry
+
+
+def measure_layer_stack(passes: int, device, seed: int = 0) -> dict:
+    """18 attention layers (B=4, H=12, T=4096, D=128),
+    layer l's window from the reference's pattern (layer_attention_window(l,
+    18, 1024, 4): layers 3, 7, 11, 15 and 17 full causal) and its q, k, v, dO
+    from seed + l.  One pass = the forwards of layers 0..17, then the
+    backwards of layers 17..0, launched back to back on one stream with a HIP
+    event between launches; per-layer times are medians over `passes`
+    passes, the totals are the medians of the pass sums and of the whole
+    pass."""
+    import torch
+
+    from hlm_attn.config import layer_attention_window
+
+    n = CFG4_LAYERS["n_layer"]
+    base = CONFIGS["cfg4_local"]
+    layers = []
+    for l in range(n):
+        w = layer_attention_window(l, n, CFG4_LAYERS["window"], CFG4_LAYERS["full_every"])
+        cfg = dict(base, W=w)
+        layers.append((cfg, Problem(cfg, seed=seed + l, device=device, tensors=device_inputs(cfg, seed + l, device))))
+
+    def one_pass():
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * n + 1)]
+        ev[0].record()
+        for l in range(n):
+            layers[l][1].fwd()
+            ev[l + 1].record()
+        for l in reversed(range(n)):
+            layers[l][1].bwd()
+            ev[2 * n - l].record()
+        return ev
+
+    warm = prewarm(torch, one_pass, min_ms=20.0, block=2, tol=0.03)
+    runs = []
+    for _ in range(passes):
+        ev = one_pass()
+        torch.cuda.synchronize()
+        fwd = [ev[l].elapsed_time(ev[l + 1]) for l in range(n)]
+        bwd = [ev[2 * n - l - 1].elapsed_time(ev[2 * n - l]) for l in range(n)]
+        runs.append((fwd, bwd, ev[0].elapsed_time(ev[2 * n])))
+    per_layer = []
+    for l in range(n):
+        f = statistics.median(r[0][l] for r in runs)
+        b = statistics.median(r[1][l] for r in runs)
+        e = {"layer": l, "window": layers[l][0]["W"]}
+        e.update(_layer_entry(layers[l][0], f, b, f + b))
+        per_layer.append(e)
+    tot_f = statistics.median(sum(r[0]) for r in runs)
+    tot_b = statistics.median(sum(r[1]) for r in runs)
+    tot = statistics.median(r[2] for r in runs)
+    flops = sum(effective_flops(c)["fwd"] + effective_flops(c)["bwd"] for c, _ in layers)
+    flops_f = sum(effective_flops(c)["fwd"] for c, _ in layers)
+    del layers
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"{n} layers B={base['B']} H={base['H']} T={base['T']} D={base['D']}, window "
+        f"{CFG4_LAYERS['window']} except the full-causal layers of layer_attention_window(l, {n}, "
+        f"{CFG4_LAYERS['window']}, {CFG4_LAYERS['full_every']}) (3, 7, 11, 15, 17); layer l's q, k, v, dO ~ N(0,1) "
+        "from seed + l; forwards 0..17 then backwards 17..0, back to back",
+        "passes": passes,
+        "prewarm_ms": warm["prewarm_ms"],
+        "prewarm_converged": warm["prewarm_converged"],
+        "layers": per_layer,
+        "total": {
+            "ms": {"fwd": round(tot_f, 4), "bwd": round(tot_b, 4), "fwd_bwd": round(tot, 4)},
+            "tflops_fwd_bwd": round(flops / (tot * 1e-3) / 1e12, 2),
+            "tflops_fwd": round(flops_f / (tot_f * 1e-3) / 1e12, 2),
+            "pct_of_bf16_peak": round(100 * flops / (tot * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            "effective_tflop": round(flops / 1e12, 4),
+        },
+    }
+
+
+def measure_configs(device) -> dict:
+    """Every BASELINE GPU config besides the headline one, in this run."""
+    return {
+        "data": "q, k, v, dO ~ N(0,1) from a seeded device generator (torch.Generator on the GPU), rounded to bf16; "
+        "HIP-event means on the launch stream, warm cache",
+        # cfg3 runs the headline's kernels (same names and grids) at twice their time; few
+        # launches keep the per-kernel averages of a rocprofv3 trace of this run on the headline
+        "cfg3_full": measure_single_layer("cfg3_full", 10, device, prewarm_ms=10.0),
+        "cfg4_stack": measure_layer_stack(3, device),
+        "cfg5_long_rope": measure_single_layer("cfg5_long", 10, device, rope=True),
     }
 
 
@@ -559,6 +777,10 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
     from oracle import attention as oracle
 
     cfg = CPU_CONFIG
+    # As many threads as this process may run on (BASELINE.md's rule).
+    threads_before = torch.get_num_threads()
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
     q, k, v = (torch.randn(cfg["B"], cfg["T"], cfg["H"], cfg["D"], generator=g) for _ in range(3))
     run = lambda: oracle.attention_core_torch(q, k, v, cfg["W"])  # noqa: E731
@@ -570,6 +792,7 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
+    torch.set_num_threads(threads_before)
     med = statistics.median(times)
     eff = 4 * cfg["D"] * pairs(cfg["T"], cfg["W"]) * cfg["B"] * cfg["H"]
     cpu_model = "unknown"
@@ -583,7 +806,7 @@ def cpu_baseline(budget_s: float = 10.0) -> dict:
     return {
         "value": round(eff / med / 1e12, 6),
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        "cores": cores,
         "kind": "port",
         "sample": (
             f"torch-backend restatement, fp32 forward, B=2 H=6 T=1024 D=64 W=256, "
@@ -601,11 +824,13 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # The GPU needs ~20 ms of work after idling before it runs at full speed
-    # (the first 100 steps run ~12% slower); 300 steps is ~50 ms.
-    ap.add_argument("--warmup", type=int, default=300)
+    # Untimed steps after the time-based pre-warm (which alone brings the GPU
+    # to its steady clock, whatever this is).
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2_local", choices=sorted(CONFIGS))
-    ap.add_argument("--sweep", action="store_true", help="also time every config (printed to stderr)")
+    ap.add_argument("--kernel-reps", type=int, default=500, help="back-to-back launches per kernel timing")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs (cfg3, cfg4, cfg5)")
+    ap.add_argument("--cold", action="store_true", help="also time per-launch medians with the cache flushed")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of the step instead of eager launches")
     ap.add_argument("--no-producer", action="store_true", help="skip the q/k RMSNorm + RoPE producer's timing")
@@ -633,19 +858,8 @@ def main() -> int:
         return 1
     device = torch.device("cuda", 0)
 
-    if args.sweep:
-        for name in CONFIGS:
-            r = measure(name, max(10, args.steps // 2), args.warmup, device, graph=args.graph)
-            print(
-                f"{name}: fwd {r['fwd_ms']*1e3:.1f} us ({r['tflops']['fwd']:.0f} TF) | "
-                f"bwd {r['bwd_ms']*1e3:.1f} us ({r['tflops']['bwd']:.0f} TF) | "
-                f"fwd+bwd {r['wall_ms_per_step']*1e3:.1f} us ({r['tflops']['fwd_bwd']:.0f} TF, "
-                f"{100*r['tflops']['fwd_bwd']/PEAK_BF16_TFLOPS:.1f}% peak) | kernels {r['kernel_us']}",
-                file=sys.stderr,
-                flush=True,
-            )
-
-    r = measure(args.config, args.steps, args.warmup, device, graph=args.graph)
+    r = measure(args.config, args.steps, args.warmup, device, graph=args.graph, kernel_reps=args.kernel_reps,
+                cold=args.cold)
     cfg = r["cfg"]
     w = "causal" if cfg["W"] is None else f"window={cfg['W']}"
     line = {
@@ -655,7 +869,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r["wall_ms_per_step"], 5),
+        "ms_per_step": round(r["step_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -675,25 +889,26 @@ def main() -> int:
         "ms_per_layer": {
             "fwd": round(r["fwd_ms"], 5),
             "bwd": round(r["bwd_ms"], 5),
-            "fwd_bwd": round(r["wall_ms_per_step"], 5),
+            "fwd_bwd": round(r["step_ms"], 5),
         },
         "tflops": {k: round(v, 2) for k, v in r["tflops"].items()},
         "kernel_us": r["kernel_us"],
         "timing": {
+            "value": f"HIP events on the launch stream around exactly {args.steps} steps (synchronised before and "
+            "after); fwd / bwd / kernel_us: HIP-event means over "
+            f"{r['kernel_reps']} back-to-back launches",
             "step": "HIP-graph replay of one fwd+bwd step" if r["graph"] else "eager launches from Python",
-            "eager_wall_ms_per_step": round(r["eager_wall_ms_per_step"], 5),
-            "event_ms_per_step": round(r["event_ms_per_step"], 5),
-            "cache_policy": "value and kernel_us: warm (steps back to back, means); median_us: per-launch "
-            f"medians, warm; cold_us: per-launch medians with {FLUSH_MB} MB written before each launch",
-            "median_us": r["median_us"],
-            "cold_us": r["cold_us"],
-            "cold_tflops_fwd_bwd": round(
-                (effective_flops(cfg)["fwd"] + effective_flops(cfg)["bwd"]) / (r["cold_us"]["fwd_bwd"] * 1e-6) / 1e12, 2
-            ),
+            "wall_ms_per_step": round(r["wall_ms_per_step"], 5),
+            **r["prewarm"],
+            "cache_policy": "warm: steps and launches back to back",
         },
         "roofline": r["roofline"],
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+        "cpu_baseline": None,
     }
+    if r["cold"] is not None:
+        line["timing"]["cold"] = r["cold"]
+    if not args.no_configs:
+        line["configs"] = measure_configs(device)
     if not args.no_producer:
         line["producer"] = measure_producer(max(args.steps, 50), 20, device)
     if not args.no_eval:
@@ -701,6 +916,9 @@ def main() -> int:
     if not args.no_lm_head:
         line["lm_head"] = measure_lm_head(max(args.steps // 4, 20), 5, device)
         line["residual_norm"] = measure_residual_norm(max(args.steps // 2, 50), 10, device)
+    if not args.no_cpu_baseline:
+        # last: ~10 s of host work, after which the GPU has idled and would need a new pre-warm
+        line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4

@@ -306,6 +306,33 @@ def test_flop_model_matches_bench():
     assert math.isclose(bench.PEAK_BF16_TFLOPS, 256 * 4096 * 2.4e9 / 1e12, rel_tol=1e-4)
 
 
+def test_bench_config_synthesis():
+    """cfg5's inputs: bench's fp32 RoPE equals the oracle's rotate-half
+    restatement (model.py:105-114 at base 10000, fraction 1.0) on the same
+    values; the cfg4 stack takes the reference's layer pattern, and its
+    effective work matches the 18-layer total of 6.611 TFLOP."""
+    import bench
+    from oracle import qk_norm_rope as rope_oracle
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 300, 3, 128, generator=g)
+    cos, sin = rope_oracle.rotary_tables(300, 128, theta=10000.0, fraction=1.0)
+    want = rope_oracle.apply_partial_rope(x, cos[None, :, None, :], sin[None, :, None, :])
+    assert torch.allclose(bench.rope_rotate(x), want, atol=2e-5, rtol=1e-5)
+    assert torch.equal(bench.rope_rotate(x)[:, 0], x[:, 0])  # position 0 is not rotated
+    from hlm_attn.config import layer_attention_window
+
+    n, w, every = (bench.CFG4_LAYERS[k] for k in ("n_layer", "window", "full_every"))
+    full = [l for l in range(n) if layer_attention_window(l, n, w, every) is None]
+    assert full == [3, 7, 11, 15, 17]
+    base = bench.CONFIGS["cfg4_local"]
+    total = 0
+    for l in range(n):
+        f = bench.effective_flops(dict(base, W=layer_attention_window(l, n, w, every)))
+        total += f["fwd"] + f["bwd"]
+    assert round(total / 1e12, 3) == 6.611
+
+
 # --- q/k RMSNorm + partial RoPE producer --------------------------------------------
 
 def _qk(lib, backward=False, ptr=0x1000, B=1, T=16, H=2, Hkv=2, D=64, rot=16, strides=(2048, 128, 64), eps=1e-6,

@@ -1,13 +1,16 @@
 """Parity of the HIP attention kernels with the fp32 oracle (GPU only).
 
-Tolerances (from the build's contract, checked here literally):
-  O         |hip - ref| <= 1e-2 + 2e-2 * |ref|    elementwise (bf16 output)
-  LSE       |hip - ref| <= 1e-3                   elementwise
-  dQ/dK/dV  |hip - ref| <= 3e-2 * (|ref| + max|ref|) + 1e-5  elementwise, i.e.
-            relative 3e-2 with the tensor's own scale as the floor for
-            near-zero entries (1e-5 absolute when the exact gradient is
-            identically zero, as at W = 1), and ||hip - ref|| / ||ref|| <= 3e-2.
-The oracle consumes the same bf16-rounded inputs upcast to fp32.
+Tolerances (north_star's numbers, checked here literally):
+  O         max |hip - ref| <= 1e-2 on its own, wherever |ref| < 2; where
+            |ref| >= 2 (windows of a few keys only: bf16's spacing there is
+            >= 2^-6) |hip - ref| <= 2e-2 |ref|; and ||hip - ref|| / ||ref|| <= 2e-2
+  LSE       max |hip - ref| <= 1e-3
+  dQ/dK/dV  ||hip - ref|| / ||ref|| <= 3e-2, and elementwise
+            |hip - ref| <= 3e-2 (|ref| + max|ref|) + 1e-5 (the tensor's own
+            scale as the floor for near-zero entries; 1e-5 absolute when the
+            exact gradient is identically zero, as at W = 1).
+Each check prints its achieved margin.  The oracle consumes the same
+bf16-rounded inputs upcast to fp32.
 """
 from __future__ import annotations
 
@@ -16,11 +19,14 @@ import math
 import pytest
 import torch
 
+import attn_checks
 from oracle import attention as oracle
+from oracle import qk_norm_rope as rope_oracle
 
 pytestmark = pytest.mark.gpu
 
 O_ATOL, O_RTOL, LSE_ATOL, GRAD_RTOL, GRAD_ATOL = 1e-2, 2e-2, 1e-3, 3e-2, 1e-5
+O_ABS_RANGE = 2.0  # |ref| below this: the max-abs bound alone applies
 
 
 def _device() -> torch.device:
@@ -29,48 +35,76 @@ def _device() -> torch.device:
     return torch.device("cuda", 0)
 
 
-def make_inputs(B, T, H, Hkv, D, seed):
-    """q, k, v, dO ~ N(0,1) from one CPU generator, rounded to bf16 (CPU)."""
+def make_inputs(B, T, H, Hkv, D, seed, rope=False):
+    """q, k, v, dO ~ N(0,1) from one CPU generator, rounded to bf16 (CPU).
+    rope=True: q and k are rotated first (rotate-half over the whole head,
+    base 10000, positions 0..T-1, in fp32), BASELINE configs[4]'s inputs."""
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, T, H, D, generator=g).bfloat16()
-    k = torch.randn(B, T, Hkv, D, generator=g).bfloat16()
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.randn(B, T, Hkv, D, generator=g)
     v = torch.randn(B, T, Hkv, D, generator=g).bfloat16()
     do = torch.randn(B, T, H, D, generator=g).bfloat16()
-    return q, k, v, do
+    if rope:
+        cos, sin = rope_oracle.rotary_tables(T, D, theta=10000.0, fraction=1.0)
+        cos, sin = cos[None, :, None, :], sin[None, :, None, :]
+        q = rope_oracle.apply_partial_rope(q, cos, sin)
+        k = rope_oracle.apply_partial_rope(k, cos, sin)
+    return q.bfloat16(), k.bfloat16(), v, do
 
 
-def run_hip(q, k, v, do, window, dev):
-    import hlm_attn
+def run_hip_device(q, k, v, do, window, dev):
+    """fwd + bwd through the custom ops; device tensors (o, lse, dq, dk, dv)."""
     from hlm_attn import ops
 
     qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
     w = 0 if window is None else window
-    o, lse = ops.hip_attn_fwd(qd, kd, vd, w, 1.0 / math.sqrt(q.shape[-1]))
-    dq, dk, dv = ops.hip_attn_bwd(dod, qd, kd, vd, o, lse, w, 1.0 / math.sqrt(q.shape[-1]))
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    o, lse = ops.hip_attn_fwd(qd, kd, vd, w, scale)
+    dq, dk, dv = ops.hip_attn_bwd(dod, qd, kd, vd, o, lse, w, scale)
     torch.cuda.synchronize()
-    return [t.float().cpu() for t in (o, lse, dq, dk, dv)]
+    return o, lse, dq, dk, dv
 
 
-def assert_out(name, got, ref):
+def run_hip(q, k, v, do, window, dev):
+    return [t.float().cpu() for t in run_hip_device(q, k, v, do, window, dev)]
+
+
+def assert_out(name, got, ref, mixed=False):
+    """mixed=False: max-abs 1e-2 alone where |ref| < 2, rel 2e-2 where
+    |ref| >= 2.  mixed=True (the sharp-score stress cases): elementwise
+    |d| <= 1e-2 + 2e-2 |ref|.  Both also bound the norm-relative error by 2e-2."""
     err = (got - ref).abs()
-    bound = O_ATOL + O_RTOL * ref.abs()
-    assert bool((err <= bound).all()), f"{name}: max err {err.max().item():.3e}, worst excess {(err - bound).max().item():.3e}"
+    small = ref.abs() < O_ABS_RANGE
+    abs_err = err[small].max().item() if bool(small.any()) else 0.0
+    big_rel = (err[~small] / ref[~small].abs()).max().item() if bool((~small).any()) else 0.0
+    rel = (err.norm() / ref.norm()).item() if ref.norm() > 0 else 0.0
+    mix = (err / (O_ATOL + O_RTOL * ref.abs())).max().item()
+    print(f"  {name}: max|d| {err.max().item():.2e} (|ref|<2: {abs_err:.2e}), rel where |ref|>=2 {big_rel:.2e}, "
+          f"max |d| / (1e-2 + 2e-2|ref|) {mix:.2f}, norm-rel {rel:.2e}", flush=True)
+    if mixed:
+        assert mix <= 1.0, f"{name}: |d| / (1e-2 + 2e-2 |ref|) reaches {mix:.3f}"
+    else:
+        assert abs_err <= O_ATOL, f"{name}: max abs err {abs_err:.3e}"
+        assert big_rel <= O_RTOL, f"{name}: max rel err where |ref| >= 2: {big_rel:.3e}"
+    assert rel <= O_RTOL, f"{name}: norm-relative error {rel:.3e}"
 
 
 def assert_lse(got, ref):
     err = (got - ref).abs().max().item()
+    print(f"  lse: max|d| {err:.2e} (<= {LSE_ATOL})", flush=True)
     assert err <= LSE_ATOL, f"lse: max err {err:.3e}"
 
 
 def assert_grad(name, got, ref):
     err = (got - ref).abs()
     scale = ref.abs().max()
+    rel = (err.norm() / ref.norm()).item() if ref.norm() > 0 else 0.0
+    print(f"  {name}: norm-rel {rel:.2e} (<= {GRAD_RTOL}), max|d| {err.max().item():.2e}, "
+          f"max|ref| {scale.item():.2e}", flush=True)
     assert bool((err <= GRAD_RTOL * (ref.abs() + scale) + GRAD_ATOL).all()), (
         f"{name}: max err {err.max().item():.3e} vs max|ref| {scale.item():.3e}"
     )
-    if ref.norm() > 0:
-        rel = (err.norm() / ref.norm()).item()
-        assert rel <= GRAD_RTOL, f"{name}: norm-relative error {rel:.3e}"
+    assert rel <= GRAD_RTOL, f"{name}: norm-relative error {rel:.3e}"
 
 
 SMALL_CASES = [
@@ -142,31 +176,61 @@ def test_tile_edge_shapes_match_oracle(B, T, H, Hkv, D, window):
 
 
 FULL_CONFIGS = [
-    # name, B, T, H, D, window  (BASELINE.json configs[1..4]; cfg4 = one local and one full layer)
-    ("cfg2_local", 8, 2048, 12, 64, 512),
-    ("cfg3_full", 8, 2048, 12, 64, None),
-    ("cfg4_local", 4, 4096, 12, 128, 1024),
-    ("cfg4_full", 4, 4096, 12, 128, None),
-    ("cfg5_long", 1, 16384, 16, 128, 2048),
+    # name, B, T, H, D, window, rope  (BASELINE.json configs[1..4]; cfg4 = one local and one full layer)
+    ("cfg2_local", 8, 2048, 12, 64, 512, False),
+    ("cfg3_full", 8, 2048, 12, 64, None, False),
+    ("cfg4_local", 4, 4096, 12, 128, 1024, False),
+    ("cfg4_full", 4, 4096, 12, 128, None, False),
+    ("cfg5_long", 1, 16384, 16, 128, 2048, False),
+    ("cfg5_long_rope", 1, 16384, 16, 128, 2048, True),  # configs[4] as stated: q, k RoPE-rotated
 ]
+BAND = 64  # queries per exact-oracle band on every (batch, head)
 
 
-@pytest.mark.parametrize("name,B,T,H,D,window", FULL_CONFIGS)
-def test_full_size_slices_match_oracle(name, B, T, H, D, window):
-    """At BASELINE sizes: exact oracle on query bands of the first and last
-    (batch, head), and size-independent invariants on the whole output."""
+@pytest.mark.parametrize("name,B,T,H,D,window,rope", FULL_CONFIGS)
+def test_full_size_slices_match_oracle(name, B, T, H, D, window, rope):
+    """At BASELINE sizes, on every (batch, head) slice: the size-independent
+    invariants of tests/attn_checks.py over the whole slice, and the exact
+    oracle (o, lse, dq) on a band of 64 queries at a slice-dependent
+    position; on the first and last slice also wide bands (window + 256
+    queries) that cover every visible key of some keys, for dk and dv."""
     dev = _device()
-    print(f"case {name} B={B} T={T} H={H} D={D} W={window}", flush=True)
-    q, k, v, do = make_inputs(B, T, H, H, D, seed=11)
-    o, lse, dq, dk, dv = run_hip(q, k, v, do, window, dev)
-    for t in (o, lse, dq, dk, dv):
+    print(f"case {name} B={B} T={T} H={H} D={D} W={window} rope={rope}", flush=True)
+    q, k, v, do = make_inputs(B, T, H, H, D, seed=11, rope=rope)
+    od, lsed, dqd, dkd, dvd = run_hip_device(q, k, v, do, window, dev)
+    for t in (od, lsed, dqd, dkd, dvd):
         assert bool(torch.isfinite(t).all())
+    inv = attn_checks.invariant_ratios(od, dkd, dvd, v.to(dev), do.to(dev), window)
+    print(f"  invariants over all {B * H} slices: dk_sum {inv['dk_sum']:.2e} (<= {attn_checks.DK_SUM_TOL}), "
+          f"dv_sum {inv['dv_sum']:.2e} (<= {attn_checks.DV_SUM_TOL}), "
+          f"o_hull {inv['o_hull']:.2e} (<= {attn_checks.O_HULL_TOL:.2e})", flush=True)
+    assert attn_checks.invariants_hold(inv), inv
+    o, lse, dq, dk, dv = (t.float().cpu() for t in (od, lsed, dqd, dkd, dvd))
+    del od, lsed, dqd, dkd, dvd
+    # every slice: one 64-query band
+    got = {"o": [], "lse": [], "dq": []}
+    ref = {"o": [], "lse": [], "dq": []}
+    for b in range(B):
+        for h in range(H):
+            q_lo = ((b * H + h) * 997 + 11) % (T - BAND + 1)
+            sl = lambda t: t[b : b + 1, :, h : h + 1]  # noqa: E731
+            ro, rlse, rdq, _, _, _ = oracle.band_forward_backward(sl(q), sl(k), sl(v), sl(do), window,
+                                                                  q_lo, q_lo + BAND)
+            got["o"].append(o[b, q_lo : q_lo + BAND, h]), ref["o"].append(ro[0, :, 0])
+            got["lse"].append(lse[b, h, q_lo : q_lo + BAND]), ref["lse"].append(rlse[0, 0])
+            got["dq"].append(dq[b, q_lo : q_lo + BAND, h]), ref["dq"].append(rdq[0, :, 0])
+    print(f"  exact oracle, one {BAND}-query band on each of the {B * H} slices:", flush=True)
+    assert_out("o", torch.stack(got["o"]), torch.stack(ref["o"]))
+    assert_lse(torch.stack(got["lse"]), torch.stack(ref["lse"]))
+    assert_grad("dq", torch.stack(got["dq"]), torch.stack(ref["dq"]))
+    # first and last slice: wide bands, dk / dv of the keys they cover completely
     w = T if window is None else window
     band = min(T, w + 256)
     for b, h in ((0, 0), (B - 1, H - 1)):
         sl = lambda t: t[b : b + 1, :, h : h + 1]  # noqa: E731
         for q_lo in sorted({0, min(T // 2 + 3, T - band), T - band}):
             q_hi = q_lo + band
+            print(f"  slice (b={b}, h={h}), queries [{q_lo}, {q_hi}):", flush=True)
             ro, rlse, rdq, rdk, rdv, k_lo = oracle.band_forward_backward(
                 sl(q), sl(k), sl(v), sl(do), window, q_lo, q_hi
             )
@@ -180,3 +244,111 @@ def test_full_size_slices_match_oracle(name, B, T, H, D, window):
                 a, z = q_lo - k_lo, k_end - k_lo
                 assert_grad("dk", dk[b : b + 1, q_lo:k_end, h : h + 1], rdk[:, a:z])
                 assert_grad("dv", dv[b : b + 1, q_lo:k_end, h : h + 1], rdv[:, a:z])
+
+
+def _fwd_c_abi(q, k, v, window, nsplit):
+    """One forward through the C ABI: hlm_attn_fwd (nsplit = 1) or
+    hlm_attn_fwd_split with a caller-owned workspace; (o, lse) on the device."""
+    from hlm_attn import _lib, ops
+
+    lib = _lib.load()
+    B, T, H, D = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
+    st = [_lib.strides3(t) for t in (q, k, v, o)]
+    w = 0 if window is None else window
+    stream = ops._stream_handle(q.device)
+    if nsplit == 1:
+        rc = lib.hlm_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              B, T, H, k.shape[2], D, *st, w, 1.0 / math.sqrt(D), stream)
+    else:
+        ws = torch.empty(nsplit * B * H * T * (D + 2), device=q.device)
+        rc = lib.hlm_attn_fwd_split(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                    ws.data_ptr(), nsplit, B, T, H, k.shape[2], D, *st, w, 1.0 / math.sqrt(D),
+                                    stream)
+    _lib.check(rc, lib)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+def sharp_inputs(B, T, H, Hkv, D, seed, kind):
+    """Scores far sharper than N(0,1) inputs give.
+    kind "scaled": q scaled by 30 (scores of ~30 nats standard deviation, a
+    row's maximum near 90 nats).
+    kind "planted": q, k ~ N(0,1) except that every query's component along a
+    unit axis u is 4 and, per kv head, three keys at T/3, 2T/3 and T - 5 are
+    100 u, 200 u and 300 u: scores of ~50, 100 and 150 nats, so a row's
+    running maximum jumps by more than 64 log2 units each time a planted
+    key's tile arrives.
+    Both drive the forward's exact rescaling path after a row's first tile."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.randn(B, T, Hkv, D, generator=g)
+    v = torch.randn(B, T, Hkv, D, generator=g)
+    if kind == "scaled":
+        q = q * 30
+    else:
+        for hk in range(Hkv):
+            ax = (5 * hk + 3) % D
+            for pos, mag in ((T // 3, 100.0), (2 * T // 3, 200.0), (T - 5, 300.0)):
+                k[:, pos, hk] = 0.0
+                k[:, pos, hk, ax] = mag
+            q[:, :, hk * (H // Hkv) : (hk + 1) * (H // Hkv), ax] = 4.0
+    return q.bfloat16(), k.bfloat16(), v.bfloat16()
+
+
+SHARP_CASES = [
+    # B, T, H, Hkv, D, window, nsplit, kind
+    (1, 700, 2, 2, 64, 300, 1, "scaled"),
+    (1, 700, 2, 2, 64, 300, 4, "scaled"),
+    (1, 700, 2, 2, 64, 300, 1, "planted"),
+    (1, 700, 2, 2, 64, 300, 4, "planted"),
+    (2, 513, 4, 2, 128, None, 1, "planted"),
+    (2, 513, 4, 2, 128, None, 3, "scaled"),
+    (1, 1000, 2, 1, 64, 97, 2, "planted"),
+]
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D,window,nsplit,kind", SHARP_CASES)
+def test_sharp_scores_forward_matches_oracle(B, T, H, Hkv, D, window, nsplit, kind):
+    """The forward's exact path (a tile whose scores exceed the running max
+    by more than 64 log2 units: tile max, rescale of O and the row sum)
+    through the one-pass and the split-key forward, against the oracle.  The
+    forward applies the softmax scale in fp32, so lse stays exact however
+    sharp the scores are.  O is held to 1e-2 + 2e-2 |ref| per element: in a
+    near-one-hot row the dominant weight is 2^(s - m) against the running
+    maximum m of the last rescale, not 1, and its bf16 rounding before the
+    P V product (up to 2^-8 relative) adds to O's own rounding (up to
+    2^-8 |O|), which can pass 1e-2 absolute at |O| near 2."""
+    dev = _device()
+    print(f"case B={B} T={T} H={H} Hkv={Hkv} D={D} W={window} nsplit={nsplit} ({kind})", flush=True)
+    q, k, v = sharp_inputs(B, T, H, Hkv, D, seed=T + nsplit, kind=kind)
+    o, lse = _fwd_c_abi(q.to(dev), k.to(dev), v.to(dev), window, nsplit)
+    ro, rlse = oracle.forward(q, k, v, window)
+    print(f"  max lse {rlse.max().item():.1f} nats", flush=True)
+    assert_out("o", o.float().cpu(), ro, mixed=True)
+    assert_lse(lse.cpu(), rlse)
+
+
+@pytest.mark.parametrize("D,window", [(64, 300), (128, None)])
+def test_sharpened_scores_backward_within_envelope(D, window):
+    """q scaled by 8 (scores up to ~40 nats): the backward holds one operand
+    of S pre-multiplied by scale * log2(e) in bf16, whose rounding error
+    grows with |S| (about 4e-4 relative gradient error per nat of the
+    largest score); at 40 nats it is well inside 3e-2.  hackable-lm's q and
+    k are RMS-normalised (model.py:101-115), so its scores never exceed
+    sqrt(D) nats."""
+    dev = _device()
+    g = torch.Generator().manual_seed(D)
+    T, H = 600, 2
+    q = (torch.randn(1, T, H, D, generator=g) * 8).bfloat16()
+    k, v, do = (torch.randn(1, T, H, D, generator=g).bfloat16() for _ in range(3))
+    print(f"case T={T} H={H} D={D} W={window} q x 8", flush=True)
+    o, lse, dq, dk, dv = run_hip(q, k, v, do, window, dev)
+    ro, rlse = oracle.forward(q, k, v, window)
+    rdq, rdk, rdv = oracle.backward(q, k, v, do, window)
+    assert_out("o", o, ro, mixed=True)  # near-one-hot rows, as in the forward's sharp cases
+    assert_lse(lse, rlse)
+    assert_grad("dq", dq, rdq)
+    assert_grad("dk", dk, rdk)
+    assert_grad("dv", dv, rdv)
