@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -24,6 +24,7 @@ SIGNATURES = {
 _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S, _S, _S, _S, _S, _S, _S, _S, _I, _F, _P]
 for _name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
     SIGNATURES[_name] = (_I, _BWD_ARGTYPES)
+SIGNATURES["hlm_attn_bwd_noalloc"] = (_I, _BWD_ARGTYPES[:9] + _BWD_ARGTYPES[10:])  # no delta_ws
 SIGNATURES["hlm_attn_fwd_split"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _S, _S, _I, _F, _P])
 SIGNATURES["hlm_attn_fwd_split_count"] = (_I, [_I, _I, _I, _I, _I])
 SIGNATURES["hlm_qk_norm_rope_fwd"] = (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])

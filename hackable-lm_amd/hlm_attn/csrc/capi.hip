@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "attn_common.h"
 #include "../../../include/hlm_attn.h"
@@ -78,7 +79,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 6; }
+int hlm_attn_abi_version(void) { return 7; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -158,21 +159,31 @@ int hlm_attn_fwd_split(const void* q, const void* k, const void* v, void* o, flo
 
 namespace {
 
-int run_bwd(int phases, const void* q, const void* k, const void* v, const void* o, const void* dout,
-            const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H, int Hkv,
-            int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-            const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
-            const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale, void* stream) {
-  g_last_error[0] = '\0';
+int check_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+              const void* dq, const void* dk, const void* dv, int B, int T, int H, int Hkv, int D,
+              const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+              const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+              const int64_t* dk_strides, const int64_t* dv_strides, float scale) {
   int rc = check_dims(B, T, H, Hkv, D, scale);
-  if (rc) return rc;
-  if (B == 0 || T == 0) return HLM_ATTN_OK;
+  if (rc || B == 0 || T == 0) return rc;
   if ((rc = check_tensor("q", q, q_strides, T, D)) || (rc = check_tensor("k", k, k_strides, T, D)) ||
       (rc = check_tensor("v", v, v_strides, T, D)) || (rc = check_tensor("o", o, o_strides, T, D)) ||
       (rc = check_tensor("dout", dout, do_strides, T, D)) || (rc = check_tensor("dq", dq, dq_strides, T, D)) ||
       (rc = check_tensor("dk", dk, dk_strides, T, D)) || (rc = check_tensor("dv", dv, dv_strides, T, D)))
     return rc;
   if (lse == nullptr) return fail(HLM_ATTN_EINVAL, "lse is a null pointer");
+  return HLM_ATTN_OK;
+}
+
+int run_bwd(int phases, const void* q, const void* k, const void* v, const void* o, const void* dout,
+            const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H, int Hkv,
+            int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+            const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale, void* stream) {
+  g_last_error[0] = '\0';
+  int rc = check_bwd(q, k, v, o, dout, lse, dq, dk, dv, B, T, H, Hkv, D, q_strides, k_strides, v_strides, o_strides,
+                     do_strides, dq_strides, dk_strides, dv_strides, scale);
+  if (rc || B == 0 || T == 0) return rc;
   if (delta_ws == nullptr) return fail(HLM_ATTN_EINVAL, "delta_ws is a null pointer");
   hlm::BwdArgs a;
   a.q = static_cast<const hlm::bf16*>(q);
@@ -207,6 +218,89 @@ int run_bwd(int phases, const void* q, const void* k, const void* v, const void*
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Allocation-free backward: the workspace of hlm_attn_bwd (-lse * log2(e) and
+// -delta per query row, 2 * B * H * T floats) lives in this file-scope device
+// array instead of caller memory.  Every device that runs the library holds
+// its own copy (32 MiB) from the module's load until the process ends.  Host
+// code never uses the array's name as an address: the device address comes
+// from hipGetSymbolAddress, once per device with that device current, and is
+// kept per device.  The dq kernel overwrites every workspace value the dkdv
+// kernel reads, so nothing needs clearing between calls; two calls that
+// overlap on one device (different streams) race on it.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchFloats = (int64_t)1 << 23;  // 32 MiB: B * H * T up to 4,194,304 query rows
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the device that owns `stream`, looked up
+// on the first call for that device (made current for the lookup).
+int scratch_for_stream(void* stream, float** out) {
+  int dev = -1;
+  hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev);
+  if (e != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(HLM_ATTN_EUNSUPPORTED, "device %d is beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess)
+      return fail(HLM_ATTN_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(HLM_ATTN_ELAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess && e2 != hipSuccess)
+        return fail(HLM_ATTN_ELAUNCH, "hipSetDevice(%d) failed: %s", cur, hipGetErrorString(e2));
+    }
+    if (e != hipSuccess || p == nullptr)
+      return fail(HLM_ATTN_ELAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return HLM_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hlm_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, void* dq, void* dk, void* dv, int B, int T, int H, int Hkv, int D,
+                         const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                         const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                         const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale,
+                         void* stream) {
+  g_last_error[0] = '\0';
+  int rc = check_bwd(q, k, v, o, dout, lse, dq, dk, dv, B, T, H, Hkv, D, q_strides, k_strides, v_strides, o_strides,
+                     do_strides, dq_strides, dk_strides, dv_strides, scale);
+  if (rc) return rc;
+  const int64_t need = 2 * (int64_t)B * H * T;
+  if (need > kScratchFloats)
+    return fail(HLM_ATTN_EUNSUPPORTED,
+                "hlm_attn_bwd_noalloc: B * H * T = %lld query rows exceeds its fixed scratch (%lld rows); "
+                "use hlm_attn_bwd with a workspace",
+                (long long)(need / 2), (long long)(kScratchFloats / 2));
+  if (B == 0 || T == 0) return HLM_ATTN_OK;
+  float* ws = nullptr;
+  if ((rc = scratch_for_stream(stream, &ws))) return rc;
+  return run_bwd(hlm::kBwdAll, q, k, v, o, dout, lse, dq, dk, dv, ws, B, T, H, Hkv, D, q_strides, k_strides,
+                 v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides, window, scale, stream);
+}
+
+}  // extern "C"
 
 #define HLM_BWD_PARAMS                                                                              \
   const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse,   \

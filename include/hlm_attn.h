@@ -144,6 +144,28 @@ int hlm_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* o
                       int window, float scale, void* stream);
 
 /*
+ * hlm_attn_bwd without the caller's workspace: the same computation and
+ * results as hlm_attn_bwd (bit for bit), with the workspace held in a
+ * fixed device array inside the library, so the call allocates nothing
+ * and needs no caller memory beyond inputs and outputs.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ * Limit: B * H * T <= 4,194,304 query rows (the array is 32 MiB per
+ * device, held from the library's load until the process ends); larger
+ * problems return HLM_ATTN_EUNSUPPORTED.  The first call on a device looks
+ * up the array's device address once.  Calls on one device share the
+ * array: calls that overlap in time on one device (on different streams)
+ * race and must not be issued; calls on one stream are ordered and safe.
+ */
+int hlm_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                         const float* lse, void* dq, void* dk, void* dv,
+                         int B, int T, int H, int Hkv, int D,
+                         const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                         const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                         const int64_t* dk_strides, const int64_t* dv_strides,
+                         int window, float scale, void* stream);
+
+/*
  * The producer step before attention: fused RMSNorm (no weight) and partial
  * rotary embedding of q and k, forward and backward.  Per (batch, time, head)
  * row x of D values, in fp32:

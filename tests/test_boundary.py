@@ -92,6 +92,24 @@ def test_bwd_phases_validate_like_bwd():
         assert rc == -2
 
 
+def test_noalloc_backward_validates_and_bounds_its_scratch_before_touching_the_device():
+    """hlm_attn_bwd_noalloc: argument errors like hlm_attn_bwd's, and problems
+    beyond its fixed scratch (B * H * T > 4,194,304 query rows) rejected with
+    a message, all before any device call."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    s = _strides(2048, 128, 64)
+    fn = lib.hlm_attn_bwd_noalloc
+    assert fn(p, p, p, p, p, p, p, p, p, 1, 16, 2, 2, 64 + 8, s, s, s, s, s, s, s, s, 0, 0.125, None) == -2
+    assert fn(p, p, p, p, p, None, p, p, p, 1, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None) == -1
+    assert b"lse" in lib.hlm_attn_last_error()
+    T, H = 65537, 64  # B * H * T = 4,194,368 rows, one row over
+    big = _strides(T * H * 64, H * 64, 64)
+    rc = fn(p, p, p, p, p, p, p, p, p, 1, T, H, H, 64, *([big] * 8), 0, 0.125, None)
+    assert rc == -2 and b"exceeds its fixed scratch" in lib.hlm_attn_last_error()
+    assert fn(p, p, p, p, p, p, p, p, p, 0, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None) == 0
+
+
 def test_split_forward_validates_and_its_policy_targets_small_grids():
     lib = _lib.load()
     s = _strides(2048, 128, 64)
