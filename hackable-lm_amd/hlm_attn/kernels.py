@@ -16,8 +16,9 @@ and semantics of the reference's `qk_norm_rope_triton` (kernels.py:756-771):
 RMSNorm of each q and k row, then the partial rotary embedding.
 
 `fused_linear_cross_entropy_with_weight(..., backend="hip")` is the LM head's
-chunked linear + cross-entropy (kernels.py:878-959) with the HIP
-cross-entropy rows in place of the Triton `linear_ce` op.
+chunked linear + cross-entropy with the signature and result of
+kernels.py:945-959: the HIP cross-entropy rows in place of the Triton
+`linear_ce` op, inside this package's own chunk loop (`_LMHeadLoss`).
 """
 from __future__ import annotations
 
@@ -184,12 +185,20 @@ def linear_ce_chunk_size(n_tokens: int, hidden_size: int, vocab_size: int, reque
     return min(n_tokens, max(chunk, LINEAR_CE_MIN_CHUNK_SIZE))
 
 
-class _HipFusedLinearCrossEntropy(torch.autograd.Function):
-    """kernels.py:878-942 with the HIP cross-entropy rows: per chunk of rows,
-    logits = hidden @ W^T (+ b) by the library GEMM, the HIP kernel turns them
-    into per-row losses and, in place, the gradient of the mean loss, and
-    the gradients of hidden, W and b are accumulated from it in the forward;
-    the backward scales them by the incoming gradient."""
+class _LMHeadLoss(torch.autograd.Function):
+    """Mean cross-entropy of hidden @ W^T (+ b), differentiable in hidden, W
+    and b, without ever holding more than one chunk of logits.
+
+    The rows are processed in chunks (`linear_ce_chunk_size`).  One logits
+    workspace of chunk x V is allocated once and every chunk's GEMM writes
+    into it; the HIP row kernel (hackable_lm::hip_linear_ce) turns it in
+    place into the gradient of the mean loss and returns the rows' losses.
+    The three gradient products are formed in the forward, straight into
+    their destinations: dhidden rows by a GEMM whose output is the chunk's
+    slice of the dhidden buffer, dW accumulated inside the GEMM (addmm_, one
+    rounding per chunk), db by an in-place add.  The backward only scales the
+    three by the incoming gradient.  The results match the reference's
+    chunked loop (kernels.py:878-942), which this replaces."""
 
     @staticmethod
     def forward(ctx, hidden, weight, targets, bias, requested_chunk_size):
@@ -198,49 +207,46 @@ class _HipFusedLinearCrossEntropy(torch.autograd.Function):
         hidden = hidden.contiguous()
         weight = weight.contiguous()
         targets = targets.contiguous()
-        n_tokens, hidden_size = hidden.shape
-        vocab_size = weight.shape[0]
-        chunk_size = linear_ce_chunk_size(n_tokens, hidden_size, vocab_size, requested_chunk_size)
-        grad_hidden = torch.empty_like(hidden)
-        grad_weight = torch.zeros_like(weight) if weight.requires_grad else None
-        grad_bias = torch.zeros_like(bias) if bias is not None and bias.requires_grad else None
-        loss_1d = torch.empty(n_tokens, dtype=torch.float32, device=hidden.device)
-        for start in range(0, n_tokens, chunk_size):
-            end = min(start + chunk_size, n_tokens)
-            hidden_chunk = hidden[start:end]
-            logits = hidden_chunk @ weight.t()
-            if bias is not None:
-                logits = logits + bias
-            logits = logits.contiguous()
-            loss_1d[start:end] = ops.hip_linear_ce(logits, targets[start:end], n_tokens)
-            grad_logits = logits
-            if hidden.requires_grad:
-                grad_hidden[start:end] = grad_logits @ weight
-            if grad_weight is not None:
-                grad_weight += torch.mm(grad_logits.t(), hidden_chunk).to(grad_weight.dtype)
-            if grad_bias is not None:
-                grad_bias += grad_logits.sum(dim=0).to(grad_bias.dtype)
-        ctx.save_for_backward(
-            grad_hidden.detach() if hidden.requires_grad else None,
-            grad_weight.detach() if grad_weight is not None else None,
-            grad_bias.detach() if grad_bias is not None else None,
-        )
-        return loss_1d.sum()
+        n, d = hidden.shape
+        vocab = weight.shape[0]
+        rows = linear_ce_chunk_size(n, d, vocab, requested_chunk_size)
+        want_h, want_w = hidden.requires_grad, weight.requires_grad
+        want_b = bias is not None and bias.requires_grad
+        d_hidden = torch.empty_like(hidden) if want_h else None
+        d_weight = torch.zeros_like(weight) if want_w else None
+        d_bias = torch.zeros_like(bias) if want_b else None
+        losses = torch.empty(n, dtype=torch.float32, device=hidden.device)
+        work = hidden.new_empty((rows, vocab))
+        w_t = weight.t()
+        for r0 in range(0, n, rows):
+            r1 = min(r0 + rows, n)
+            h = hidden[r0:r1]
+            g = work[: r1 - r0]
+            if bias is None:
+                torch.mm(h, w_t, out=g)
+            else:
+                torch.addmm(bias, h, w_t, out=g)
+            losses[r0:r1] = ops.hip_linear_ce(g, targets[r0:r1], n)
+            if want_h:
+                torch.mm(g, weight, out=d_hidden[r0:r1])
+            if want_w:
+                d_weight.addmm_(g.t(), h)
+            if want_b:
+                d_bias.add_(g.sum(dim=0).to(d_bias.dtype))
+        ctx.save_for_backward(d_hidden, d_weight, d_bias)
+        return losses.sum()
 
     @staticmethod
     def backward(ctx, grad_output):
-        grad_hidden, grad_weight, grad_bias = ctx.saved_tensors
-
-        def scaled(g):
-            return None if g is None else g * grad_output.to(dtype=g.dtype)
-
-        return (
-            scaled(grad_hidden) if ctx.needs_input_grad[0] else None,
-            scaled(grad_weight) if ctx.needs_input_grad[1] else None,
-            None,
-            scaled(grad_bias) if ctx.needs_input_grad[3] else None,
-            None,
-        )
+        d_hidden, d_weight, d_bias = ctx.saved_tensors
+        out = []
+        for need, t in ((ctx.needs_input_grad[0], d_hidden), (ctx.needs_input_grad[1], d_weight)):
+            out.append(t * grad_output.to(t.dtype) if need and t is not None else None)
+        out.append(None)
+        need_b = ctx.needs_input_grad[3] and d_bias is not None
+        out.append(d_bias * grad_output.to(d_bias.dtype) if need_b else None)
+        out.append(None)
+        return tuple(out)
 
 
 def fused_linear_cross_entropy_with_weight(
@@ -261,7 +267,7 @@ def fused_linear_cross_entropy_with_weight(
     targets_flat = targets.reshape(-1).contiguous()
     if hidden_flat.device.type != "cuda":
         raise RuntimeError("the hip fused linear cross entropy runs on ROCm devices only")
-    return _HipFusedLinearCrossEntropy.apply(hidden_flat, weight, targets_flat, bias, chunk_size)
+    return _LMHeadLoss.apply(hidden_flat, weight, targets_flat, bias, chunk_size)
 
 
 # --- residual add + RMSNorm (OutputProjection / DownProjection) --------------------
