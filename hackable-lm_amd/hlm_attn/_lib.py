@@ -68,6 +68,25 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     return lib
 
 
+_pycall = None
+
+
+def load_pycall():
+    """The CPython binding of the forward entry points (_pycall, built with the
+    library by hlm_attn.build and linked against it); raises if it is missing."""
+    global _pycall
+    if _pycall is None:
+        load()  # the library first: a missing or stale build raises here
+        try:
+            from . import _pycall as mod
+        except ImportError as e:
+            raise HipAttentionUnavailable(
+                f"the CPython binding next to {LIB_PATH} is missing ({e}): build it with `python -m hlm_attn.build`"
+            ) from e
+        _pycall = mod
+    return _pycall
+
+
 _Strides = ctypes.c_int64 * 3
 _strides_cache: dict = {}
 

@@ -1,7 +1,8 @@
-"""Builds libhlm_attn.so (the HIP kernels + C ABI) for gfx950 with hipcc.
+"""Builds libhlm_attn.so (the HIP kernels + C ABI) for gfx950 with hipcc, and
+the CPython binding of its forward entry points (_pycall, host code, g++).
 
-The library is built in-tree next to this file, so it travels with the source
-tree to the GPU host.  Usage:  python -m hlm_attn.build  (or build()).
+Both are built in-tree next to this file, so they travel with the source tree
+to the GPU host.  Usage:  python -m hlm_attn.build  (or build()).
 """
 from __future__ import annotations
 
@@ -9,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 import tempfile
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
@@ -18,6 +20,7 @@ CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libhlm_attn.so"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
 ARCH = "gfx950"
+PYCALL_PATH = PKG_DIR / ("_pycall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code.
 HIPCC_FLAGS = [
@@ -78,7 +81,22 @@ def build(verbose: bool = False, out: Path | None = None, defines: tuple[str, ..
     if verbose and log.strip():
         print(log, file=sys.stderr)
     os.replace(tmp, target)
+    if out is None:
+        build_pycall()
     return target
+
+
+def build_pycall() -> Path:
+    """Compiles csrc/pycall.cpp (CPython API, no device code) into PYCALL_PATH,
+    linked against LIB_PATH in the same directory."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) for the CPython binding")
+    tmp = PYCALL_PATH.with_name(PYCALL_PATH.name + ".tmp")
+    _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+          str(CSRC / "pycall.cpp"), f"-L{PKG_DIR}", "-lhlm_attn", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
+    os.replace(tmp, PYCALL_PATH)
+    return PYCALL_PATH
 
 
 if __name__ == "__main__":

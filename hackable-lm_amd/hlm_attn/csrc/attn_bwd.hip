@@ -201,8 +201,8 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   const bool wave_live = qw0 < T;
   const int wq_hi = min(qw0 + 31, T - 1);
   // D = 64 issues all S and dP operand reads of a tile at once (the registers
-  // for that fit with 3 waves per SIMD); D = 128 reads them as it goes.
-  constexpr bool kBatchReads = D == 64;
+  // for that fit with 3 waves per SIMD) and keeps the start values splatted;
+  // D = 128 reads the operands as it goes.
   [[maybe_unused]] const f32x16 slse = splat16(nlse2), sdel = splat16(ndelta);
 
   // D = 64 synchronises every second tile (tiles it and it + 1 behind one

@@ -77,23 +77,23 @@ def attention(
     k leave q.k unchanged, zero columns of v only add zero output columns
     (sliced off), and the scale stays 1/sqrt(Dqk).  Gradients flow back
     through the padding exactly."""
-    from . import ops  # registers the custom ops on first use
-
-    if q.dtype != torch.bfloat16:
-        q = q.to(torch.bfloat16)
-    if k.dtype != torch.bfloat16:
-        k = k.to(torch.bfloat16)
-    if v.dtype != torch.bfloat16:
-        v = v.to(torch.bfloat16)
+    ops = _ops or _load_ops()
+    bf16 = torch.bfloat16
+    if q.dtype is not bf16:
+        q = q.to(bf16)
+    if k.dtype is not bf16:
+        k = k.to(bf16)
+    if v.dtype is not bf16:
+        v = v.to(bf16)
+    dqk, dv = q.shape[-1], v.shape[-1]
     if scale is None:
-        scale = 1.0 / math.sqrt(q.shape[-1])
+        scale = 1.0 / math.sqrt(dqk)
     if window_size is not None and window_size < 1:
         raise RuntimeError(f"window_size must be >= 1 or None, got {window_size}")
     window = 0 if window_size is None else int(window_size)
-    dqk, dv = q.shape[-1], v.shape[-1]
     if k.shape[-1] != dqk:
         raise RuntimeError(f"q head dim {dqk} and k head dim {k.shape[-1]} differ")
-    d_kernel = padded_head_dim(dqk, dv)
+    d_kernel = dqk if dqk == dv and (dqk == 64 or dqk == 128) else padded_head_dim(dqk, dv)
     if d_kernel != dqk or d_kernel != dv:
         pad = torch.nn.functional.pad
         q, k = pad(q, (0, d_kernel - dqk)), pad(k, (0, d_kernel - dqk))
@@ -103,6 +103,18 @@ def attention(
     else:
         out, _ = ops.hip_attn_fwd(q, k, v, window, float(scale))
     return out if d_kernel == dv else out[..., :dv]
+
+
+_ops = None
+
+
+def _load_ops():
+    """hlm_attn.ops, imported (which registers the custom ops) on first use."""
+    global _ops
+    from . import ops
+
+    _ops = ops
+    return ops
 
 
 def padded_head_dim(dqk: int, dv: int) -> int:

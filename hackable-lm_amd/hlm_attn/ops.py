@@ -22,36 +22,38 @@ from . import _lib
 _BF16 = torch.bfloat16
 
 
+def _layout_ok(t: torch.Tensor, s: tuple) -> bool:
+    """t (strides s) fits the kernels: unit D stride, (batch, time, head)
+    strides multiples of 8 elements, non-overlapping rows, 16-byte aligned."""
+    return s[3] == 1 and not (s[0] | s[1] | s[2]) & 7 and s[1] >= t.shape[3] and not t.data_ptr() & 15
+
+
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """Returns t if its layout fits the kernels (unit D stride, 16-byte aligned,
-    non-overlapping rows), else a contiguous copy."""
-    s = t.stride()
-    ok = (
-        s[3] == 1
-        and all(x >= 0 and x % 8 == 0 for x in s[:3])
-        and s[1] >= t.shape[3]
-        and t.data_ptr() % 16 == 0
-    )
-    return t if ok else t.contiguous()
+    """Returns t if its layout fits the kernels, else a contiguous copy."""
+    return t if _layout_ok(t, t.stride()) else t.contiguous()
 
 
 def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    qs, ks = q.shape, k.shape
+    if (q.is_cuda and q.dtype is _BF16 and k.dtype is _BF16 and v.dtype is _BF16 and len(qs) == 4
+            and len(ks) == 4 and ks == v.shape and qs[0] == ks[0] and qs[1] == ks[1] and qs[3] == ks[3]
+            and ks[2] > 0 and qs[2] % ks[2] == 0 and q.get_device() == k.get_device() == v.get_device()):
+        return  # the common case, checked without building device objects
     dev = q.device
     if dev.type != "cuda":
         raise RuntimeError(f"hip attention runs on ROCm devices only, got a tensor on {dev}")
-    if not (q.dtype == k.dtype == v.dtype == _BF16 and q.dim() == k.dim() == v.dim() == 4
-            and k.device == dev and v.device == dev):
-        for name, t in (("q", q), ("k", k), ("v", v)):
-            if t.dtype != _BF16:
-                raise RuntimeError(f"hip attention expects bfloat16 {name}, got {t.dtype}")
-            if t.dim() != 4:
-                raise RuntimeError(f"hip attention expects {name} shaped (B, T, H, D), got {tuple(t.shape)}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != _BF16:
+            raise RuntimeError(f"hip attention expects bfloat16 {name}, got {t.dtype}")
+        if t.dim() != 4:
+            raise RuntimeError(f"hip attention expects {name} shaped (B, T, H, D), got {tuple(t.shape)}")
+    if k.device != dev or v.device != dev:
         raise RuntimeError("q, k and v must be on the same device")
     if k.shape != v.shape:
         raise RuntimeError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must have the same shape")
     if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
         raise RuntimeError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree on B, T or D")
-    if q.shape[2] % k.shape[2] != 0:
+    if k.shape[2] == 0 or q.shape[2] % k.shape[2] != 0:
         raise RuntimeError(f"query heads {q.shape[2]} are not a multiple of kv heads {k.shape[2]}")
 
 
@@ -66,12 +68,26 @@ def _stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _raw_stream_of(index: int) -> int:
+    """_stream_handle's value as a Python int, for a device index."""
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
 def _on_device(device: torch.device):
     """Makes `device` current for the launch; a no-op (and no device guard's
     cost) when it already is."""
     if device.index is None or device.index == torch.cuda.current_device():
         return contextlib.nullcontext()
     return torch.cuda.device(device)
+
+
+def _on_index(index: int):
+    """_on_device for a device index (tensor.get_device())."""
+    if index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(index)
 
 
 def direct_call_ok(*tensors: torch.Tensor) -> bool:
@@ -92,42 +108,52 @@ def direct_call_ok(*tensors: torch.Tensor) -> bool:
 def attn_fwd_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """The forward launch behind hackable_lm::hip_attn_fwd (o, lse)."""
+    """The forward launch behind hackable_lm::hip_attn_fwd (o, lse), through
+    the CPython binding of the C ABI (one C call; the per-call host cost
+    matters at batch 1 and short T, where the kernel takes a few us)."""
     _check_inputs(q, k, v)
-    lib = _lib.load()
-    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    pycall = _lib._pycall or _lib.load_pycall()
+    sq, sk, sv = q.stride(), k.stride(), v.stride()
+    if not _layout_ok(q, sq):
+        q = q.contiguous()
+        sq = q.stride()
+    if not _layout_ok(k, sk):
+        k = k.contiguous()
+        sk = k.stride()
+    if not _layout_ok(v, sv):
+        v = v.contiguous()
+        sv = v.stride()
     B, T, H, D = q.shape
-    o = torch.empty((B, T, H, D), dtype=_BF16, device=q.device)
-    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
-    nsplit = split_count(lib, B, T, H, D, int(window))
-    strides = (_lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o))
-    with _on_device(q.device):
-        if nsplit > 1:  # small grid: split each query tile's keys, then merge (evaluation-sized calls)
-            ws = torch.empty(nsplit * B * H * T * (D + 2), dtype=torch.float32, device=q.device)
-            rc = lib.hlm_attn_fwd_split(
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), ws.data_ptr(), nsplit,
-                B, T, H, k.shape[2], D, *strides, int(window), float(scale), _stream_handle(q.device),
-            )
-        else:
-            rc = lib.hlm_attn_fwd(
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                B, T, H, k.shape[2], D, *strides, int(window), float(scale), _stream_handle(q.device),
-            )
-    _lib.check(rc, lib)
+    o = q.new_empty((B, T, H, D))
+    lse = q.new_empty((B, H, T), dtype=torch.float32)
+    window = int(window)
+    nsplit = _split_cache.get((B, T, H, D, window)) or split_count(B, T, H, D, window)
+    # small grid: split each query tile's keys, then merge (evaluation-sized calls)
+    ws = q.new_empty(nsplit * B * H * T * (D + 2), dtype=torch.float32) if nsplit > 1 else None
+    idx = q.get_device()
+    with _on_index(idx):
+        rc = pycall.fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            0 if ws is None else ws.data_ptr(), nsplit, B, T, H, k.shape[2], D,
+            sq[0], sq[1], sq[2], sk[0], sk[1], sk[2], sv[0], sv[1], sv[2], T * H * D, H * D, D,
+            window, float(scale), _raw_stream_of(idx),
+        )
+    if rc != 0:
+        _lib.check(rc, _lib.load())
     return o, lse
 
 
 _split_cache: dict = {}
 
 
-def split_count(lib, B: int, T: int, H: int, D: int, window: int) -> int:
+def split_count(B: int, T: int, H: int, D: int, window: int) -> int:
     """hlm_attn_fwd_split_count, memoised per shape."""
     key = (B, T, H, D, window)
     n = _split_cache.get(key)
     if n is None:
         if len(_split_cache) > 4096:
             _split_cache.clear()
-        n = _split_cache[key] = lib.hlm_attn_fwd_split_count(B, T, H, D, window)
+        n = _split_cache[key] = _lib.load().hlm_attn_fwd_split_count(B, T, H, D, window)
     return n
 
 

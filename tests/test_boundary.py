@@ -73,6 +73,34 @@ def test_fwd_rejects_bad_arguments_before_touching_the_device(kwargs, code, msg)
     assert msg in lib.hlm_attn_last_error().decode()
 
 
+def test_cpython_binding_passes_the_same_arguments_to_the_c_abi():
+    """_pycall.fwd (the no-grad host path) reaches the same validation as the
+    ctypes call: same codes, same messages, no device touched; the split
+    entry point behind nsplit > 1 too."""
+    lib = _lib.load()
+    pc = _lib.load_pycall()
+    st = (2048, 128, 64) * 4
+
+    def call(ptr=0x1000, nsplit=1, ws=0, D=64, H=2, Hkv=2, window=0, scale=0.125, strides=st):
+        return pc.fwd(ptr, ptr, ptr, ptr, 0x2000, ws, nsplit, 1, 16, H, Hkv, D, *strides, window, scale, 0)
+
+    for kwargs, code, msg in [
+        (dict(D=96), -2, "head_dim 96"),
+        (dict(H=3, Hkv=2), -1, "not a multiple"),
+        (dict(ptr=0), -1, "null pointer"),
+        (dict(ptr=0x1008), -1, "16-byte aligned"),
+        (dict(strides=(2048, 100, 64) * 4), -1, "multiple of 8"),
+        (dict(scale=float("nan")), -1, "scale"),
+        (dict(nsplit=4, ws=0), -1, "workspace"),
+    ]:
+        assert call(**kwargs) == code, kwargs
+        assert msg in lib.hlm_attn_last_error().decode(), kwargs
+    with pytest.raises(TypeError):
+        pc.fwd(1, 2, 3)
+    with pytest.raises(TypeError):
+        call(scale="x")
+
+
 def test_empty_problems_are_no_ops():
     lib = _lib.load()
     assert _fwd(lib, B=0) == 0
