@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   constexpr int TILEB = BMQ * D * 2;     // bytes of one Q or dO tile
   constexpr int SLOTB = 2 * TILEB;       // one ring slot: Q and dO
   constexpr int CPT = TILEB / 1024;      // 1 KB chunks per tile
-  constexpr int PER = 2 * CPT / NW;      // bf16 DMA instructions per wave per tile (+1 on waves 0, 1)
+  constexpr int PER = 2 * CPT / NW + 1;  // DMA instructions per wave per tile: Q and dO pieces, one start-value row
   constexpr int NCH = 32 / L::RPC;       // chunks of a wave's 32 rows
   constexpr int WSTG = 2 * NCH * 1024;   // staging bytes per wave (K and V)
   // D = 64: K and V rows arrive by whole-row DMA into ring slots and are read
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   static_assert(!STAGE_KV || PRE * SLOTB + NW * WSTG <= NBUF * SLOTB, "staging fits behind the first tiles");
   static_assert(PRE >= 2 && PRE < NBUF, "tiles 0 and 1 are in flight before the loop");
   static_assert(NBUF >= 4, "a barrier every second tile needs two tiles of slack");
-  static_assert(NBUF * (PER + 1) < 64 && 2 * NS + 2 * NCH + PRE * (PER + 1) < 64, "vmcnt range");
+  static_assert(NBUF * PER < 64 && 2 * NS + 2 * NCH + PRE * PER < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char ring[NBUF * SLOTB];
   __shared__ __attribute__((aligned(256))) float stbuf[NBUF][128];  // [0, 64): -lse * log2(e), [64, 128): -delta
 
@@ -439,7 +439,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   const int n_iter = nq * G;
   const int sq2 = (int)(a.sq[1] * 2), sdo2 = (int)(a.sdo[1] * 2);
 
-  const unsigned lring = lds_addr(ring), lst = lds_addr(stbuf) + 256 * wave;
+  // Start values: waves 0 and 2 copy a tile's -lse*log2(e) row, waves 1 and 3
+  // its -delta row, to the same LDS bytes (identical data), so every wave
+  // issues the same number of copies per tile and waits on one count.
+  const unsigned lring = lds_addr(ring), lst = lds_addr(stbuf) + 256 * (wave & 1);
   const unsigned stg_k = lring + PRE * SLOTB + wave * WSTG, stg_v = stg_k + NCH * 1024;
 
   // 1. This wave's K and V rows: into the staging area (cs layout), or
@@ -469,15 +472,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   // 2. Query tiles, visited head by head (the G query heads of this kv head),
   // tile by tile; each copy goes to ring slot (issue index) % NBUF.  The
   // buffer resources walk down the slabs by one tile per copy.
-  int ld_g = 0, ld_t = 0, issued = 0;
-  const int64_t qstep = (int64_t)BMQ * a.sq[1] * 2, dostep = (int64_t)BMQ * a.sdo[1] * 2;
-  const int64_t plane = wave == 0 ? 0 : (int64_t)(a.B * H) * T;  // waves 0 / 1 copy -lse*log2(e) / -delta
-  SlabCursor cq, cdo, cst;
+  int ld_g = 0, ld_t = 0, issued = 0, islot = 0;
+  const int qstep = BMQ * sq2, dostep = BMQ * sdo2;  // bytes per query tile (< 2^31: the host bounds each slab)
+  const int64_t plane = (wave & 1) == 0 ? 0 : (int64_t)(a.B * H) * T;  // -lse*log2(e) or -delta rows
+  // Per query head: buffer resources over its Q, dO and workspace rows from
+  // row tq_lo * BMQ on (reads past the last row return zeros); a tile's copy
+  // adds only its byte offset to each lane's fixed offset.
+  __amdgpu_buffer_rsrc_t rq, rdo, rst;
   auto start_head = [&]() __attribute__((always_inline)) {
     const int hq = hk * G + ld_g, qs = tq_lo * BMQ;
-    cq = slab_cursor(a.q + b * a.sq[0] + hq * a.sq[2], a.sq[1], T, D, qs);
-    cdo = slab_cursor(a.dout + b * a.sdo[0] + hq * a.sdo[2], a.sdo[1], T, D, qs);
-    cst = {(uint64_t)(uintptr_t)(a.delta + plane + ((int64_t)b * H + hq) * T + qs), (int64_t)(T - qs) * 4};
+    rq = slab_rsrc(a.q + b * a.sq[0] + hq * a.sq[2] + (int64_t)qs * a.sq[1], a.sq[1], T - qs, D);
+    rdo = slab_rsrc(a.dout + b * a.sdo[0] + hq * a.sdo[2] + (int64_t)qs * a.sdo[1], a.sdo[1], T - qs, D);
+    rst = row_rsrc(a.delta + plane + ((int64_t)b * H + hq) * T + qs, T - qs);
   };
   start_head();
   int qof[CPT / NW], dof[CPT / NW];
@@ -488,35 +494,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     dof[i] = L::dma_row(j, lane) * sdo2 + L::dma_col_bytes(j, lane);
   }
   auto load_tile = [&]() __attribute__((always_inline)) {
-    const int slot = issued % NBUF;
-    const unsigned sb = lring + (unsigned)slot * SLOTB;
-    const __amdgpu_buffer_rsrc_t rq = cq.rsrc(), rdo = cdo.rsrc();
+    const unsigned sb = lring + (unsigned)islot * SLOTB;
+    const int tq = ld_t * qstep, tdo = ld_t * dostep;
 #pragma unroll
     for (int i = 0; i < CPT / NW; ++i) {
       const unsigned piece = (unsigned)(wave + NW * i) * 1024;
-      lds_dma_at<16>(rq, sb + piece, qof[i]);
-      lds_dma_at<16>(rdo, sb + TILEB + piece, dof[i]);
+      lds_dma_at<16>(rq, sb + piece, qof[i] + tq);
+      lds_dma_at<16>(rdo, sb + TILEB + piece, dof[i] + tdo);
     }
-    if (wave < 2) lds_dma_at<4>(cst.rsrc(), lst + slot * 512, lane * 4);  // fp32 rows, 64 lanes x 4 bytes
+    lds_dma_at<4>(rst, lst + islot * 512, lane * 4 + ld_t * (BMQ * 4));  // fp32 rows, 64 lanes x 4 bytes
     ++issued;
+    islot = islot == NBUF - 1 ? 0 : islot + 1;
     if (++ld_t == nq) {
       ld_t = 0;
       ++ld_g;
       if (ld_g < G) start_head();
-    } else {
-      cq.advance(qstep);
-      cdo.advance(dostep);
-      cst.advance(BMQ * 4);
     }
   };
   const int n_pre = min(PRE, n_iter);
   for (int i = 0; i < n_pre; ++i) load_tile();
 
   // 3. Wait for this wave's K and V rows (the first tiles may be in flight).
-  if (wave < 2)
-    vm_wait_upto<PER + 1, PRE>(n_pre);
-  else
-    vm_wait_upto<PER, PRE>(n_pre);
+  vm_wait_upto<PER, PRE>(n_pre);
 
   // Operand offsets: kept in registers for D = 64, recomputed per use for
   // D = 128 (whose accumulators leave no room for them).
@@ -594,13 +593,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // the staging area); then the ring is topped up to NBUF - 1 tiles past
     // it.  Tile it + 1 then needs no barrier of its own.
     if ((slot & 1) == 0) {
-      const int need = min(it + 1, n_iter - 1);
-      if (wave < 2)
-        dma_barrier_upto<PER + 1, NBUF - 1>(issued - 1 - need);
-      else
+      if (it >= 2 && it + NBUF <= n_iter) {
+        // Steady state: tiles it + 2 .. it + NBUF - 3 stay in flight behind
+        // tiles it and it + 1, and the two slots just freed take tiles
+        // it + NBUF - 2 and it + NBUF - 1.
+        static_assert(NBUF % 2 == 0 && NBUF >= 4, "groups of two tiles fill the ring");
+        dma_barrier<(NBUF - 4) * PER>();
+        load_tile();
+        load_tile();
+      } else {
+        const int need = min(it + 1, n_iter - 1);
         dma_barrier_upto<PER, NBUF - 1>(issued - 1 - need);
-      const int want = min(it + NBUF, n_iter);
-      while (issued < want) load_tile();
+        const int want = min(it + NBUF, n_iter);
+        while (issued < want) load_tile();
+      }
     }
 
     const unsigned qs_t = lbase + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
