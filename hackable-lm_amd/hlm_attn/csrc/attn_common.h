@@ -167,28 +167,6 @@ __device__ __forceinline__ void lds_dma_at(__amdgpu_buffer_rsrc_t rs, unsigned l
     asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(ldsaddr));
 }
 
-// A buffer resource that walks down a slab tile by tile: `addr` is the byte
-// address of the current tile's first row and `bytes` the bytes left in the
-// slab from there (<= 0 past the end: every read returns zeros).
-struct SlabCursor {
-  uint64_t addr;
-  int64_t bytes;
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
-    const int n = bytes > 0 ? (int)bytes : 0;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, n, 0x00020000);
-  }
-  __device__ __forceinline__ void advance(int64_t step) {
-    addr += step;
-    bytes -= step;
-  }
-};
-
-// Cursor over a (batch, head) slab of T rows of 2*D bytes at row stride st
-// elements, positioned at row r0.
-__device__ __forceinline__ SlabCursor slab_cursor(const bf16* base, int64_t st, int T, int D, int r0) {
-  return {(uint64_t)(uintptr_t)(base + (int64_t)r0 * st), (int64_t)(T - 1 - r0) * st * 2 + 2 * D};
-}
-
 // Barrier for tiles that arrive by LDS DMA: wait until at most `pending` of
 // this wave's vector-memory ops are outstanding (the DMA of newer tiles,
 // which complete after the older ones), drain LDS ops, then s_barrier.  A
