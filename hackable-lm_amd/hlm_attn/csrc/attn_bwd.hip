@@ -470,8 +470,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   }
 
   // 2. Query tiles, visited head by head (the G query heads of this kv head),
-  // tile by tile; each copy goes to ring slot (issue index) % NBUF.  The
-  // buffer resources walk down the slabs by one tile per copy.
+  // tile by tile; each copy goes to ring slot (issue index) % NBUF.
   int ld_g = 0, ld_t = 0, issued = 0, islot = 0;
   const int qstep = BMQ * sq2, dostep = BMQ * sdo2;  // bytes per query tile (< 2^31: the host bounds each slab)
   const int64_t plane = (wave & 1) == 0 ? 0 : (int64_t)(a.B * H) * T;  // -lse*log2(e) or -delta rows
