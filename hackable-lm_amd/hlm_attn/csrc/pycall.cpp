@@ -9,6 +9,7 @@
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
+#include <climits>
 #include <cstdint>
 
 #include "../../../include/hlm_attn.h"
@@ -32,19 +33,29 @@ PyObject* py_fwd(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   }
   void* ptr[6];
   for (int i = 0; i < 6; ++i) ptr[i] = PyLong_AsVoidPtr(args[i]);
-  const long nsplit = PyLong_AsLong(args[6]);
-  int dims[5];
-  for (int i = 0; i < 5; ++i) dims[i] = (int)PyLong_AsLong(args[7 + i]);
+  // nsplit, B, T, H, Hkv, D and window are C ints: out-of-range values raise
+  // instead of wrapping into a different, valid-looking problem.
+  int ints[7];
+  for (int i = 0; i < 7; ++i) {
+    const long v = PyLong_AsLong(args[i == 6 ? 24 : 6 + i]);
+    if (v == -1 && PyErr_Occurred()) return nullptr;
+    if (v < INT_MIN || v > INT_MAX) {
+      PyErr_Format(PyExc_OverflowError, "fwd argument %d (%ld) does not fit a C int", i == 6 ? 24 : 6 + i, v);
+      return nullptr;
+    }
+    ints[i] = (int)v;
+  }
+  const int nsplit = ints[0], window = ints[6];
+  const int* dims = ints + 1;
   int64_t st[4][3];
   for (int i = 0; i < 12; ++i) st[i / 3][i % 3] = (int64_t)PyLong_AsLongLong(args[12 + i]);
-  const int window = (int)PyLong_AsLong(args[24]);
   const float scale = (float)PyFloat_AsDouble(args[25]);
   void* stream = PyLong_AsVoidPtr(args[26]);
   if (PyErr_Occurred()) return nullptr;
   int rc;
   if (nsplit > 1)
     rc = hlm_attn_fwd_split(ptr[0], ptr[1], ptr[2], ptr[3], static_cast<float*>(ptr[4]), static_cast<float*>(ptr[5]),
-                            (int)nsplit, dims[0], dims[1], dims[2], dims[3], dims[4], st[0], st[1], st[2], st[3],
+                            nsplit, dims[0], dims[1], dims[2], dims[3], dims[4], st[0], st[1], st[2], st[3],
                             window, scale, stream);
   else
     rc = hlm_attn_fwd(ptr[0], ptr[1], ptr[2], ptr[3], static_cast<float*>(ptr[4]), dims[0], dims[1], dims[2],

@@ -99,6 +99,8 @@ def test_cpython_binding_passes_the_same_arguments_to_the_c_abi():
         pc.fwd(1, 2, 3)
     with pytest.raises(TypeError):
         call(scale="x")
+    with pytest.raises(OverflowError):  # a C int argument out of range raises rather than wrapping
+        call(H=2**32 + 2, Hkv=2)
 
 
 def test_empty_problems_are_no_ops():
