@@ -87,6 +87,26 @@ def load_pycall():
     return _pycall
 
 
+_torch_fwd = None
+
+
+def load_torch_fwd():
+    """The torch C++ extension of the no-grad forward (_torch_fwd: checks,
+    allocation and launch in one call), built with the library; raises if it
+    is missing."""
+    global _torch_fwd
+    if _torch_fwd is None:
+        load()
+        try:
+            from . import _torch_fwd as mod
+        except ImportError as e:
+            raise HipAttentionUnavailable(
+                f"the torch extension next to {LIB_PATH} is missing ({e}): build it with `python -m hlm_attn.build`"
+            ) from e
+        _torch_fwd = mod
+    return _torch_fwd
+
+
 _Strides = ctypes.c_int64 * 3
 _strides_cache: dict = {}
 

@@ -1,5 +1,6 @@
-"""Builds libhlm_attn.so (the HIP kernels + C ABI) for gfx950 with hipcc, and
-the CPython binding of its forward entry points (_pycall, host code, g++).
+"""Builds libhlm_attn.so (the HIP kernels + C ABI) for gfx950 with hipcc, the
+CPython binding of its forward entry points (_pycall, host code, g++) and the
+torch C++ extension of the no-grad forward (_torch_fwd, host code).
 
 Both are built in-tree next to this file, so they travel with the source tree
 to the GPU host.  Usage:  python -m hlm_attn.build  (or build()).
@@ -21,6 +22,7 @@ LIB_PATH = PKG_DIR / "libhlm_attn.so"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
 ARCH = "gfx950"
 PYCALL_PATH = PKG_DIR / ("_pycall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+TORCH_FWD_PATH = PKG_DIR / "_torch_fwd.so"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code.
 HIPCC_FLAGS = [
@@ -83,6 +85,7 @@ def build(verbose: bool = False, out: Path | None = None, defines: tuple[str, ..
     os.replace(tmp, target)
     if out is None:
         build_pycall()
+        build_torch_fwd()
     return target
 
 
@@ -97,6 +100,30 @@ def build_pycall() -> Path:
           str(CSRC / "pycall.cpp"), f"-L{PKG_DIR}", "-lhlm_attn", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
     os.replace(tmp, PYCALL_PATH)
     return PYCALL_PATH
+
+
+
+def build_torch_fwd() -> Path:
+    """Compiles csrc/torch_fwd.cpp (torch C++ extension, host code only) into
+    TORCH_FWD_PATH with g++ and torch's headers, linked against torch and
+    against LIB_PATH in the same directory."""
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) for the torch extension")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-w",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=_torch_fwd", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *[f"-I{d}" for d in cpp_extension.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "torch_fwd.cpp"),
+           *[f"-L{d}" for d in cpp_extension.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           f"-L{PKG_DIR}", "-lhlm_attn", "-Wl,-rpath,$ORIGIN"]
+    tmp = TORCH_FWD_PATH.with_name(TORCH_FWD_PATH.name + ".tmp")
+    _run([*cmd, "-o", str(tmp)])
+    os.replace(tmp, TORCH_FWD_PATH)
+    return TORCH_FWD_PATH
 
 
 if __name__ == "__main__":

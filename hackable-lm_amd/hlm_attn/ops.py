@@ -108,9 +108,17 @@ def direct_call_ok(*tensors: torch.Tensor) -> bool:
 def attn_fwd_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """The forward launch behind hackable_lm::hip_attn_fwd (o, lse), through
-    the CPython binding of the C ABI (one C call; the per-call host cost
-    matters at batch 1 and short T, where the kernel takes a few us)."""
+    """The forward launch behind hackable_lm::hip_attn_fwd (o, lse).  Inputs
+    already in the kernels' layout go through the torch extension, which
+    checks, allocates and launches in one C++ call (the per-call host cost
+    matters at batch 1 and short T, where the kernel takes a few us); the
+    rest are checked, copied to that layout where needed, and launched
+    through the CPython binding of the same C ABI."""
+    ext = _lib._torch_fwd or _lib.load_torch_fwd()
+    if q.is_cuda:
+        res = ext.fwd(q, k, v, int(window), float(scale), _raw_stream_of(q.get_device()))
+        if res:
+            return res[0], res[1]
     _check_inputs(q, k, v)
     pycall = _lib._pycall or _lib.load_pycall()
     sq, sk, sv = q.stride(), k.stride(), v.stride()

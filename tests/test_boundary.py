@@ -103,6 +103,18 @@ def test_cpython_binding_passes_the_same_arguments_to_the_c_abi():
         call(H=2**32 + 2, Hkv=2)
 
 
+def test_torch_extension_takes_only_kernel_ready_device_inputs():
+    """_torch_fwd.fwd (the no-grad fast path) hands back [] for anything it
+    does not launch itself -- here CPU tensors, wrong dtypes, wrong ranks or
+    mismatched shapes -- so the caller's general path converts or raises."""
+    ext = _lib.load_torch_fwd()
+    q = torch.zeros(1, 16, 2, 64, dtype=torch.bfloat16)
+    assert ext.fwd(q, q, q, 0, 0.125, 0) == []
+    assert ext.fwd(q.float(), q.float(), q.float(), 0, 0.125, 0) == []
+    assert ext.fwd(q[0], q[0], q[0], 0, 0.125, 0) == []
+    assert ext.fwd(q, q[:, :8], q[:, :8], 0, 0.125, 0) == []
+
+
 def test_empty_problems_are_no_ops():
     lib = _lib.load()
     assert _fwd(lib, B=0) == 0
