@@ -56,8 +56,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
     const int heads = a.heads[w];
     const int bt = r / heads, h = r - bt * heads;
     const int b = bt / a.T, t = bt - b * a.T;
-    xv = *reinterpret_cast<const bf16x8*>(a.x[w] + b * a.s[w][0] + t * a.s[w][1] + h * a.s[w][2] + 8 * c);
-    if constexpr (BWD) gv = *reinterpret_cast<const bf16x8*>(a.g[w] + (int64_t)r * D + 8 * c);
+    const bf16x8* xp = reinterpret_cast<const bf16x8*>(a.x[w] + b * a.s[w][0] + t * a.s[w][1] + h * a.s[w][2] + 8 * c);
+    // Non-temporal loads measured 4% faster in the backward and 13% slower in
+    // the forward (whose rows are strided views of the fused projection).
+    xv = BWD ? __builtin_nontemporal_load(xp) : *xp;
+    if constexpr (BWD) gv = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(a.g[w] + (int64_t)r * D + 8 * c));
     if (rotary) {
       const int64_t cb = (int64_t)t * a.rot + (8 * c) % half;
       const Tab* cp = static_cast<const Tab*>(a.cos) + cb;

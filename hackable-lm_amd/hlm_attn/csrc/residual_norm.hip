@@ -12,7 +12,8 @@
 // of 8 values (16 bytes) at elements 8 (lane + 64 j), so each wave
 // instruction moves 1 KB of one row, coalesced; the row's sums are wave
 // shuffles (no LDS, no barrier).  Forward: 2 reads + 2 writes of 2n bytes
-// per row; backward: 3 reads + 1 write.
+// per row; backward: 3 reads + 1 write.  Every byte is touched once, so loads
+// and stores are non-temporal (12% faster than cached ones on the MI355X).
 #include "attn_common.h"
 
 namespace hlm {
@@ -47,9 +48,9 @@ __global__ __launch_bounds__(256) void residual_rms_norm_kernel(ResNormArgs p) {
     const int e0 = 8 * (lane + 64 * j);
     va[j] = vb[j] = vc[j] = bf16x8{};
     if (e0 < n) {
-      va[j] = *reinterpret_cast<const bf16x8*>(p.a + base + e0);
-      vb[j] = *reinterpret_cast<const bf16x8*>(p.b + base + e0);
-      if constexpr (BWD) vc[j] = *reinterpret_cast<const bf16x8*>(p.c + base + e0);
+      va[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p.a + base + e0));
+      vb[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p.b + base + e0));
+      if constexpr (BWD) vc[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p.c + base + e0));
     }
   }
   if constexpr (!BWD) {
@@ -70,8 +71,8 @@ __global__ __launch_bounds__(256) void residual_rms_norm_kernel(ResNormArgs p) {
       bf16x8 z;
 #pragma unroll
       for (int e = 0; e < 8; ++e) z[e] = (bf16)((float)va[j][e] * r);
-      *reinterpret_cast<bf16x8*>(p.y0 + base + e0) = va[j];
-      *reinterpret_cast<bf16x8*>(p.y1 + base + e0) = z;
+      __builtin_nontemporal_store(va[j], reinterpret_cast<bf16x8*>(p.y0 + base + e0));
+      __builtin_nontemporal_store(z, reinterpret_cast<bf16x8*>(p.y1 + base + e0));
     }
   } else {
     float ss = 0.f, dot = 0.f;
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void residual_rms_norm_kernel(ResNormArgs p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         g[e] = (bf16)((float)vb[j][e] + fmaf(r, (float)vc[j][e], -k * (float)va[j][e]));
-      *reinterpret_cast<bf16x8*>(p.y0 + base + e0) = g;
+      __builtin_nontemporal_store(g, reinterpret_cast<bf16x8*>(p.y0 + base + e0));
     }
   }
 }
