@@ -66,7 +66,7 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 //  * O is read with coalesced loads (whole rows per instruction) only to form
 //    delta = rowsum(dO * O) together with the staged dO.
 //  * dQ leaves through LDS: each wave writes its 32 x D block into a cs tile
-//    and stores whole rows.
+//    and stores whole rows (non-temporal).
 // Tile and staging copies are inline asm with explicit waits; the few loads
 // into registers are ordinary (compiler-tracked) buffer loads issued before
 // them, and no store is issued before the loop ends, so inside the loop the
@@ -374,7 +374,8 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   for (int k = 0; k < NCH; ++k) {
     const int row = L::dma_row(k, ln);
     const bf16x8 v = lds_read_b128(reg + L::byte(row, ln % L::U));
-    if (qw0 + row < T) *reinterpret_cast<bf16x8*>(dqbase + (int64_t)(qw0 + row) * a.sdq[1] + 8 * (ln % L::U)) = v;
+    bf16x8* dst = reinterpret_cast<bf16x8*>(dqbase + (int64_t)(qw0 + row) * a.sdq[1] + 8 * (ln % L::U));
+    if (qw0 + row < T) __builtin_nontemporal_store(v, dst);
   }
   if (myq < T && h32 == 0) {
     a.delta[(int64_t)bh * T + myq] = nlse2;
@@ -693,8 +694,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int row = L::dma_row(k, ln), ub = L::byte(row, ln % L::U);
     const bf16x8 kv = lds_read_b128(rk_ + ub), vv = lds_read_b128(rv_ + ub);
     if (kw0 + row < T) {
-      *reinterpret_cast<bf16x8*>(dkbase + (int64_t)(kw0 + row) * a.sdk[1] + 8 * (ln % L::U)) = kv;
-      *reinterpret_cast<bf16x8*>(dvbase + (int64_t)(kw0 + row) * a.sdv[1] + 8 * (ln % L::U)) = vv;
+      const int64_t r = kw0 + row;
+      __builtin_nontemporal_store(kv, reinterpret_cast<bf16x8*>(dkbase + r * a.sdk[1] + 8 * (ln % L::U)));
+      __builtin_nontemporal_store(vv, reinterpret_cast<bf16x8*>(dvbase + r * a.sdv[1] + 8 * (ln % L::U)));
     }
   }
 }
