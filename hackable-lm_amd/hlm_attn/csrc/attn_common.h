@@ -81,12 +81,32 @@ struct BwdArgs {
 };
 
 // Arguments of the fused q/k RMSNorm + partial rotary kernels (qk_norm_rope.hip).
+// Division of 0 <= n < 2^31 by a fixed divisor 1 <= d < 2^31 as a multiply
+// and a shift (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994, Thm. 4.2): with l = ceil(log2 d), p = 31 + l and
+// mul = ceil(2^p / d) (< 2^32), floor(n / d) = (n * mul) >> p, because
+// 2^p <= mul d < 2^p + 2^(p - 31).  The host fills it (fast_div_of).
+struct FastDiv {
+  unsigned mul;
+  int shift;  // p
+};
+__host__ __device__ inline FastDiv fast_div_of(unsigned d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  const int p = 31 + l;
+  return {(unsigned)(((1ull << p) + d - 1) / d), p};
+}
+__host__ __device__ __forceinline__ int fast_div(int n, FastDiv f) {
+  return (int)(((unsigned long long)(unsigned)n * f.mul) >> f.shift);
+}
+
 struct QkNormRopeArgs {
   const bf16* x[2];   // q, k: (B, T, heads, D), unit D stride
   const bf16* g[2];   // backward: gradients of the two outputs, contiguous
   bf16* out[2];       // outputs (forward) or input gradients (backward), contiguous
   int64_t s[2][3];    // (batch, time, head) strides of q and k in elements
   int heads[2];       // H, Hkv
+  FastDiv div_heads[2], div_T;  // the same divisors for the row -> (batch, time, head) split
   const void* cos;    // (T, R) rows, fp32 or bf16 (tab_bf16); columns 0 .. R / 2 - 1 are read
   const void* sin;
   int tab_bf16;

@@ -358,6 +358,9 @@ int run_qk_norm_rope(bool backward, const void* q, const void* k, const void* gq
   copy3(a.s[1], k_strides);
   a.heads[0] = H;
   a.heads[1] = Hkv;
+  a.div_heads[0] = hlm::fast_div_of((unsigned)H);
+  a.div_heads[1] = hlm::fast_div_of((unsigned)Hkv);
+  a.div_T = hlm::fast_div_of((unsigned)T);
   a.cos = cos;
   a.sin = sin;
   a.tab_bf16 = table_dtype == HLM_TABLE_BF16;

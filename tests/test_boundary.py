@@ -609,3 +609,24 @@ def test_other_head_dims_run_zero_padded(fake_op):
         kernels.attention(torch.randn(1, 5, 2, 192), torch.randn(1, 5, 2, 192), torch.randn(1, 5, 2, 192))
     with pytest.raises(RuntimeError, match="differ"):
         kernels.attention(torch.randn(1, 5, 2, 64), torch.randn(1, 5, 2, 32), torch.randn(1, 5, 2, 64))
+
+
+# --- host-side arithmetic shared with the kernels ----------------------------
+
+def test_fast_division_matches_integer_division(tmp_path):
+    """The producer splits its row index into (batch, time, head) by
+    multiply-high division (attn_common.h: FastDiv); fastdiv_check.cpp runs
+    that same code on the host against the compiler's integer division over
+    184 M (dividend, divisor) pairs, range ends included."""
+    import shutil
+    import subprocess
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "fastdiv_check"
+    src = REPO / "tests" / "fastdiv_check.cpp"
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950", str(src), "-o", str(exe)],
+                   check=True, capture_output=True, timeout=300)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
