@@ -120,10 +120,15 @@ __global__ __launch_bounds__(256) void ce_rows_vec_kernel(CeArgs a) {
     u32x4 outw;
     T* o = reinterpret_cast<T*>(&outw);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float g = fast_exp2(fmaf(to_f32(v[e]), kLog2e, -c)) * scale;
-      if (status == 0 && idx + e == tgt) g -= a.inv_n;
-      o[e] = (T)g;
+    for (int e = 0; e < E; ++e) o[e] = (T)(fast_exp2(fmaf(to_f32(v[e]), kLog2e, -c)) * scale);
+    // The target's gradient, p_t / S - 1 / n, rounded once as above: one test
+    // per chunk instead of one per element (the lane holding the target redoes
+    // its element; the others skip the branch).
+    if (status == 0 && (uint64_t)(tgt - idx) < (uint64_t)E) {
+      const int et = (int)(tgt - idx);
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (e == et) o[e] = (T)(fast_exp2(fmaf(to_f32(v[e]), kLog2e, -c)) * scale - a.inv_n);
     }
     *reinterpret_cast<u32x4*>(base + idx) = outw;
   }
