@@ -114,6 +114,7 @@ struct QkNormRopeArgs {
   float eps;
   int rows_q;  // B * T * H
   int rows;    // B * T * (H + Hkv), < 2^31
+  int blocks_q;  // workgroups of q rows (set by the launcher)
 };
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {

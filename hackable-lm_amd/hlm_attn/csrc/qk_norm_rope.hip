@@ -30,6 +30,44 @@
 
 namespace hlm {
 
+// Cross-lane moves inside a row's lanes by DPP (no LDS round trip):
+// quad_perm [1,0,3,2] is lane ^ 1, [2,3,0,1] lane ^ 2; row_half_mirror maps
+// lane i of each 8 to 7 - i, row_mirror lane i of each 16 to 15 - i.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// Sum over each aligned group of G = 8 or 16 lanes, every lane getting it:
+// after the two quad steps each lane holds its quad's sum, and a mirror
+// pairs every lane with one of the other quad (then of the other 8).  The
+// additions pair the same values as a lane ^ 1, ^ 2, ^ 4 (, ^ 8) butterfly.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G == 8 || G == 16, "rows of 8 or 16 lanes");
+  v += dpp_mov<kDppXor1>(v);
+  v += dpp_mov<kDppXor2>(v);
+  v += dpp_mov<kDppHalfMirror>(v);
+  if constexpr (G == 16) v += dpp_mov<kDppMirror>(v);
+  return v;
+}
+
+// The rotation partner's value: lane ^ 1 (R = 16) or lane ^ 2 (R = 32) by
+// DPP, otherwise lane +- R / 16 through the LDS crossbar.
+__device__ __forceinline__ void partner_values(const float (&v)[8], float (&out)[8], int hp, int partner) {
+  if (hp == 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = dpp_mov<kDppXor1>(v[e]);
+  } else if (hp == 2) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = dpp_mov<kDppXor2>(v[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = __shfl(v[e], partner);
+  }
+}
+
 template <int D, bool BWD, typename Tab>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
   constexpr int LPR = D / 8;       // lanes per row
@@ -40,19 +78,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
   const bool rotary = 8 * c < a.rot;
   const bool low = 8 * c < half;
   const int partner = lane + (low ? half / 8 : -(half / 8));  // same row (R % 16 == 0)
-  const int row = (int)blockIdx.x * RPB + tid / LPR;          // < 2^31 (checked by the host)
-  const bool live = row < a.rows;
+  // q rows take the first blocks_q workgroups, k rows the rest, so which
+  // tensor a workgroup serves is uniform and its arguments are scalar loads.
+  const int w = (int)blockIdx.x >= a.blocks_q;
+  const int r = ((int)blockIdx.x - (w ? a.blocks_q : 0)) * RPB + tid / LPR;  // < 2^31 (checked by the host)
+  const bool live = r < (w ? a.rows - a.rows_q : a.rows_q);
 
   // 1. Loads: the row's 8 values, its gradient (backward), and for rotary
   //    lanes cos / sin at columns (8 c) mod h .. + 7 of time step t.
-  bf16x8 xv{}, gv{};
-  float cs[8], sn[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) cs[e] = sn[e] = 0.f;
-  int w = 0, r = 0;
+  // The table rows stay raw until they are used, so that all of a lane's
+  // loads are in flight together.
+  bf16x8 xv{}, gv{}, c8{}, s8{};
+  f32x4 c0{}, c1{}, s0{}, s1{};
   if (live) {
-    w = row >= a.rows_q;
-    r = w ? row - a.rows_q : row;
     // r -> (bt, h) -> (b, t) by multiply-high division: the compiler's
     // division by a runtime value sits in front of every load (8% of the
     // forward's time).
@@ -68,22 +106,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
       const Tab* cp = static_cast<const Tab*>(a.cos) + cb;
       const Tab* sp = static_cast<const Tab*>(a.sin) + cb;
       if constexpr (sizeof(Tab) == 2) {
-        const bf16x8 c8 = *reinterpret_cast<const bf16x8*>(cp), s8 = *reinterpret_cast<const bf16x8*>(sp);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          cs[e] = (float)c8[e];
-          sn[e] = (float)s8[e];
-        }
+        c8 = *reinterpret_cast<const bf16x8*>(cp);
+        s8 = *reinterpret_cast<const bf16x8*>(sp);
       } else {
-        const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp), c1 = *reinterpret_cast<const f32x4*>(cp + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          cs[e] = c0[e];
-          cs[e + 4] = c1[e];
-          sn[e] = s0[e];
-          sn[e + 4] = s1[e];
-        }
+        c0 = *reinterpret_cast<const f32x4*>(cp);
+        c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+        s0 = *reinterpret_cast<const f32x4*>(sp);
+        s1 = *reinterpret_cast<const f32x4*>(sp + 4);
       }
     }
   }
@@ -97,14 +126,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
     x[e] = (float)xv[e];
     ss = fmaf(x[e], x[e], ss);
   }
-#pragma unroll
-  for (int m = 1; m < LPR; m <<= 1) ss += __shfl_xor(ss, m);
+  ss = group_sum<LPR>(ss);
   const float inv = rsqrtf(ss * (1.f / D) + a.eps);
+  float cs[8], sn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (sizeof(Tab) == 2) {
+      cs[e] = (float)c8[e];
+      sn[e] = (float)s8[e];
+    } else {
+      cs[e] = e < 4 ? c0[e & 3] : c1[e & 3];
+      sn[e] = e < 4 ? s0[e & 3] : s1[e & 3];
+    }
+  }
+  const int hp = half / 8;
   float res[8];
   if constexpr (!BWD) {
     float xp[8];  // the partner's raw values (same row, same inv)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xp[e] = __shfl(x[e], partner);
+    partner_values(x, xp, hp, partner);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float z = x[e] * inv;
@@ -119,8 +158,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
     float g[8], gp[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[e] = (float)gv[e];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) gp[e] = __shfl(g[e], partner);
+    partner_values(g, gp, hp, partner);
     float gn[8], dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -131,8 +169,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkNormRopeArgs a) {
       }
       dot = fmaf(gn[e], x[e] * inv, dot);
     }
-#pragma unroll
-    for (int m = 1; m < LPR; m <<= 1) dot += __shfl_xor(dot, m);
+    dot = group_sum<LPR>(dot);
     dot *= 1.f / D;
 #pragma unroll
     for (int e = 0; e < 8; ++e) res[e] = inv * (gn[e] - x[e] * inv * dot);
@@ -159,10 +196,12 @@ hipError_t launch_typed(const QkNormRopeArgs& a, unsigned blocks, hipStream_t st
 template <int D>
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream) {
   constexpr int RPB = 256 / (D / 8);
-  const int64_t blocks = ((int64_t)a.rows + RPB - 1) / RPB;
+  QkNormRopeArgs b = a;
+  b.blocks_q = (int)(((int64_t)a.rows_q + RPB - 1) / RPB);
+  const int64_t blocks = b.blocks_q + ((int64_t)(a.rows - a.rows_q) + RPB - 1) / RPB;
   if (blocks == 0) return hipSuccess;
-  return backward ? launch_typed<D, true>(a, (unsigned)blocks, stream)
-                  : launch_typed<D, false>(a, (unsigned)blocks, stream);
+  return backward ? launch_typed<D, true>(b, (unsigned)blocks, stream)
+                  : launch_typed<D, false>(b, (unsigned)blocks, stream);
 }
 
 template hipError_t launch_qk_norm_rope<64>(const QkNormRopeArgs&, bool, hipStream_t);
