@@ -377,31 +377,49 @@ def measure_eval(reps: int, device) -> dict:
     hlm_attn.attention (which skips the op dispatcher when nothing needs
     autograd).  Per shape and window: `call_us`, HIP-event time per call over
     back-to-back calls (host and GPU overlapped, what an evaluation loop
-    sees); `kernel_us`, the same through the C ABI alone (GPU-bound); the
-    split count the library chose."""
+    sees); `kernel_us`, the same launches (split-key when the library splits)
+    through the C ABI alone (GPU-bound); the split count the library chose."""
     import torch
 
     import hlm_attn
 
+    def warm(fn, min_ms=30.0):
+        # Back-to-back calls until the GPU has run min_ms of them (the clock
+        # ramps up under load; a fixed count of short calls does not get there).
+        done = 0.0
+        while done < min_ms:
+            done += event_time_ms(torch, fn, 10) * 10
+
     lib = None
-    out = {"workload": "no-grad forwards, H=12 D=64, windows 512 and causal; synthetic N(0,1) bf16", "shapes": []}
+    out = {"workload": "no-grad forwards, H=12 D=64, windows 512 and causal; synthetic N(0,1) bf16",
+           "timing": "each path warmed for >= 30 ms of GPU time, then HIP events around `reps` back-to-back calls",
+           "shapes": []}
     for B, T in EVAL_SHAPES:
         for W in (512, None):
             cfg = dict(B=B, T=T, H=12, D=64, W=W)
             prob = Problem(cfg, seed=0, device=device)
             lib = prob.lib
+            nsplit = lib.hlm_attn_fwd_split_count(B, T, 12, 64, 0 if W is None else W)
             call = lambda: hlm_attn.attention(prob.q, prob.k, prob.v, window_size=W)  # noqa: E731
             with torch.no_grad():
-                for _ in range(20):
-                    call()
+                warm(call)
                 call_ms = event_time_ms(torch, call, reps)
-            for _ in range(20):
-                prob.fwd()
-            kern_ms = event_time_ms(torch, prob.fwd, reps)
+            kernel = prob.fwd
+            if nsplit > 1:  # the same split-key launches the call path makes
+                ws = torch.empty(nsplit * B * 12 * T * (64 + 2), dtype=torch.float32, device=device)
+
+                def kernel():
+                    rc = lib.hlm_attn_fwd_split(
+                        prob.q.data_ptr(), prob.k.data_ptr(), prob.v.data_ptr(), prob.o.data_ptr(), prob.lse.data_ptr(),
+                        ws.data_ptr(), nsplit, *prob.dims, prob.s["q"], prob.s["k"], prob.s["v"], prob.s["o"],
+                        prob.window, prob.scale, prob.stream)
+                    assert rc == 0, lib.hlm_attn_last_error()
+            warm(kernel)
+            kern_ms = event_time_ms(torch, kernel, reps)
             fl = 4 * cfg["D"] * pairs(T, W) * B * cfg["H"]
             out["shapes"].append({
                 "B": B, "T": T, "window": W,
-                "nsplit": lib.hlm_attn_fwd_split_count(B, T, 12, 64, 0 if W is None else W),
+                "nsplit": nsplit,
                 "call_us": round(call_ms * 1e3, 2),
                 "kernel_us": round(kern_ms * 1e3, 2),
                 "tflops": round(fl / (call_ms * 1e-3) / 1e12, 1),
