@@ -35,9 +35,11 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kNonTemporal = 2;  // cache-policy operand of the buffer builtins: nt
 constexpr int kThreads = 256;  // 4 waves of 64
 
 // Backward phases (bit mask): dQ + delta first, then dK/dV, which reads delta.
@@ -164,6 +166,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16* base, int64_t st, int T, int D) {
   const int64_t extent = (int64_t)(T - 1) * st * 2 + 2 * D;  // bytes; < 2^31 (checked by the host)
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
+}
+
+// Raw buffer of `extent` bytes at `base`: loads past the end return zeros and
+// stores past it are dropped.  Built from uniform values it costs a few
+// scalar instructions, so loops can move a tile's row offset into the base
+// (slab_rsrc from a later row) and keep their per-lane offsets invariant.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bytes_rsrc(const void* base, int extent) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, extent, 0x00020000);
 }
 
 // LDS byte address of a __shared__ location (taken once per kernel; the

@@ -74,9 +74,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   const int q0 = qt * BM, qw0 = q0 + 32 * wave;
 
   const __amdgpu_buffer_rsrc_t rq = slab_rsrc(a.q + b * a.sq[0] + h * a.sq[2], a.sq[1], T, D);
-  const __amdgpu_buffer_rsrc_t rk = slab_rsrc(a.k + b * a.sk[0] + hk * a.sk[2], a.sk[1], T, D);
-  const __amdgpu_buffer_rsrc_t rv = slab_rsrc(a.v + b * a.sv[0] + hk * a.sv[2], a.sv[1], T, D);
+  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk[0] + hk * a.sk[2]);
+  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv[0] + hk * a.sv[2]);
   const int sq2 = (int)(a.sq[1] * 2), sk2 = (int)(a.sk[1] * 2), sv2 = (int)(a.sv[1] * 2);
+  // Slab extents in bytes (< 2^31, checked by the host): rows >= T read as zeros.
+  const int kext = (T - 1) * sk2 + 2 * D, vext = (T - 1) * sv2 + 2 * D;
 
   const unsigned lring = lds_addr(ring);
   const unsigned stg_q = lring + PRE * SLOTB + wave * WSTG;
@@ -106,22 +108,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   for (int k = 0; k < NCH; ++k)
     lds_dma_at<16>(rq, stg_q + k * 1024, (qw0 + L::dma_row(k, lane)) * sq2 + L::dma_col_bytes(k, lane));
 
-  // 2. The first key tiles.
+  // 2. The first key tiles.  A tile's buffer descriptors start at its first
+  // row (scalar arithmetic), so the per-lane offsets are loop-invariant
+  // registers (opaque: not recomputed in the loop) and rows >= T still read
+  // as zeros.
   int kof[CPT / NW], vof[CPT / NW];
 #pragma unroll
   for (int i = 0; i < CPT / NW; ++i) {
     const int j = wave + NW * i;
     kof[i] = L::dma_row(j, lane) * sk2 + L::dma_col_bytes(j, lane);
     vof[i] = L::dma_row(j, lane) * sv2 + L::dma_col_bytes(j, lane);
+    asm volatile("" : "+v"(kof[i]), "+v"(vof[i]));
   }
   auto load_tile = [&](int t) __attribute__((always_inline)) {
     const unsigned slot = lring + (unsigned)(t % NBUF) * SLOTB;
-    const int kb = (t_lo + t) * BN * sk2, vb = (t_lo + t) * BN * sv2;
+    const int row0 = (t_lo + t) * BN;  // < T
+    const int kskip = row0 * sk2, vskip = row0 * sv2;
+    const __amdgpu_buffer_rsrc_t rk = bytes_rsrc(kslab + kskip, kext - kskip);
+    const __amdgpu_buffer_rsrc_t rv = bytes_rsrc(vslab + vskip, vext - vskip);
 #pragma unroll
     for (int i = 0; i < CPT / NW; ++i) {
       const unsigned piece = (unsigned)(wave + NW * i) * 1024;
-      lds_dma_at<16>(rk, slot + piece, kb + kof[i]);
-      lds_dma_at<16>(rv, slot + TILEB + piece, vb + vof[i]);
+      lds_dma_at<16>(rk, slot + piece, kof[i]);
+      lds_dma_at<16>(rv, slot + TILEB + piece, vof[i]);
     }
   };
   const int n_pre = min(PRE, n_tiles);
@@ -284,12 +293,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
 
   // O through LDS (whole rows leave with coalesced stores, non-temporal: 1-3%
   // faster than cached ones, here and for dQ, dK, dV); lse from lanes 0..31.
+  // O is rounded to bf16, so a 1-ulp reciprocal of the row sum suffices.
   dma_barrier<0>();
   int ln = lane;
   asm volatile("" : "+v"(ln));  // epilogue addresses are computed here, not hoisted above the loop
   const int e32 = ln & 31, eh = ln >> 5;
   const float ltot = lsum + __shfl_xor(lsum, 32);
-  const float inv = 1.f / ltot;
+  const float inv = __builtin_amdgcn_rcpf(ltot);
   const unsigned reg = lring + wave * (32 * D * 2);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -300,13 +310,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
       for (int j = 0; j < 4; ++j) v4[j] = (bf16)(oacc[db][4 * i + j] * inv);
       lds_write_b64(reg + L::byte(e32, 4 * db + i) + 8 * eh, v4);
     }
-  bf16* obase = a.o + b * a.so[0] + h * a.so[2];
+  if (wave_live) {
+    // The wave's rows from qw0 on; stores to rows >= T fall past the buffer's
+    // end and are dropped.
+    const int so2 = (int)(a.so[1] * 2);
+    const __amdgpu_buffer_rsrc_t ro =
+        bytes_rsrc(a.o + b * a.so[0] + h * a.so[2] + (int64_t)qw0 * a.so[1], (T - 1 - qw0) * so2 + 2 * D);
 #pragma unroll
-  for (int k = 0; k < NCH; ++k) {
-    const int row = L::dma_row(k, ln);
-    const bf16x8 v = lds_read_b128(reg + L::byte(row, ln % L::U));
-    bf16x8* dst = reinterpret_cast<bf16x8*>(obase + (int64_t)(qw0 + row) * a.so[1] + 8 * (ln % L::U));
-    if (qw0 + row < T) __builtin_nontemporal_store(v, dst);
+    for (int k = 0; k < NCH; ++k) {
+      const int row = L::dma_row(k, ln);
+      const bf16x8 v = lds_read_b128(reg + L::byte(row, ln % L::U));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, row * so2 + 16 * (ln % L::U), 0,
+                                             kNonTemporal);
+    }
   }
   const int myq = qw0 + l32;
   if (myq < T && h32 == 0) a.lse[(int64_t)bh * T + myq] = (m + __log2f(ltot)) * kLn2;
