@@ -87,24 +87,46 @@ def load_pycall():
     return _pycall
 
 
-_torch_fwd = None
+_torch_fwd = None  # the extension module once loaded; False once a load failed or it is disabled
+_torch_fwd_error = ""
 
 
 def load_torch_fwd():
     """The torch C++ extension of the no-grad forward (_torch_fwd: checks,
-    allocation and launch in one call), built with the library; raises if it
-    is missing."""
-    global _torch_fwd
+    allocation and launch in one C++ call), built with the library; raises if
+    it is missing or unusable.  The forward does not need it: see torch_fwd()."""
+    ext = torch_fwd()
+    if ext is None:
+        raise HipAttentionUnavailable(
+            f"the torch extension next to {LIB_PATH} is unavailable ({_torch_fwd_error}): "
+            "build it with `python -m hlm_attn.build`"
+        )
+    return ext
+
+
+def torch_fwd():
+    """The optional torch C++ extension of the forward, or None.
+
+    It only saves host time per call (a few microseconds at batch 1); every
+    forward also runs through the C ABI without it.  None when it is missing,
+    when it was built against another torch (its import then fails), or when
+    HLM_ATTN_TORCH_EXT=0 disables it.  The first failure is remembered, so the
+    import is attempted once per process."""
+    global _torch_fwd, _torch_fwd_error
     if _torch_fwd is None:
-        load()
-        try:
-            from . import _torch_fwd as mod
-        except ImportError as e:
-            raise HipAttentionUnavailable(
-                f"the torch extension next to {LIB_PATH} is missing ({e}): build it with `python -m hlm_attn.build`"
-            ) from e
-        _torch_fwd = mod
-    return _torch_fwd
+        import os
+
+        if os.environ.get("HLM_ATTN_TORCH_EXT", "1") == "0":
+            _torch_fwd, _torch_fwd_error = False, "disabled by HLM_ATTN_TORCH_EXT=0"
+        else:
+            try:
+                load()
+                from . import _torch_fwd as mod
+            except (ImportError, OSError, HipAttentionUnavailable) as e:
+                _torch_fwd, _torch_fwd_error = False, f"{type(e).__name__}: {e}"
+            else:
+                _torch_fwd = mod
+    return _torch_fwd or None
 
 
 _Strides = ctypes.c_int64 * 3

@@ -32,11 +32,15 @@ from .config import HIP_BACKEND, normalize_attention_backend
 
 
 def hip_attention_available() -> bool:
-    """True when a ROCm device is visible and libhlm_attn.so loads."""
+    """True when a ROCm device is visible and every module the forward and
+    backward need loads: libhlm_attn.so (the kernels and the C ABI) and its
+    CPython binding.  The torch extension of the forward is optional (a host
+    fast path) and is not required here."""
     if not torch.cuda.is_available() or torch.version.hip is None:
         return False
     try:
         _lib.load()
+        _lib.load_pycall()
     except (_lib.HipAttentionUnavailable, OSError):
         return False
     return True

@@ -109,13 +109,17 @@ def attn_fwd_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The forward launch behind hackable_lm::hip_attn_fwd (o, lse).  Inputs
-    already in the kernels' layout go through the torch extension, which
-    checks, allocates and launches in one C++ call (the per-call host cost
-    matters at batch 1 and short T, where the kernel takes a few us); the
-    rest are checked, copied to that layout where needed, and launched
-    through the CPython binding of the same C ABI."""
-    ext = _lib._torch_fwd or _lib.load_torch_fwd()
-    if q.is_cuda:
+    are checked, copied to the kernels' layout where needed, and launched
+    through the CPython binding of the C ABI.  When the optional torch
+    extension is present, inputs already in the kernels' layout take it
+    instead: it checks, allocates and launches in one C++ call, which matters
+    at batch 1 and short T, where the kernel takes a few us.  Without it (not
+    built, built against another torch, or disabled) the results are the
+    same: both paths launch the same kernels through the same C entry points."""
+    ext = _lib._torch_fwd
+    if ext is None:
+        ext = _lib.torch_fwd()
+    if ext and q.is_cuda:
         res = ext.fwd(q, k, v, int(window), float(scale), _raw_stream_of(q.get_device()))
         if res:
             return res[0], res[1]

@@ -355,6 +355,74 @@ def test_resolution_follows_the_reference_rules(monkeypatch):
         kernels.resolve_attention_backend("sdpa")
 
 
+class _FakePycall:
+    """Stands in for the CPython binding: records the forward's arguments."""
+
+    def __init__(self):
+        self.calls = []
+
+    def fwd(self, *args):
+        self.calls.append(args)
+        return 0
+
+
+@pytest.mark.parametrize("how", ["env", "import"])
+def test_forward_falls_back_to_the_c_abi_without_the_torch_extension(monkeypatch, how):
+    """The torch extension is an optional host fast path: when it is disabled
+    (HLM_ATTN_TORCH_EXT=0) or its import fails (missing, or built against
+    another torch), torch_fwd() is None, the failure is cached, and
+    attn_fwd_impl launches through the CPython binding of the C ABI with the
+    same arguments."""
+    import sys
+
+    monkeypatch.setattr(_lib, "_torch_fwd", None)
+    if how == "env":
+        monkeypatch.setenv("HLM_ATTN_TORCH_EXT", "0")
+    else:
+        monkeypatch.delenv("HLM_ATTN_TORCH_EXT", raising=False)
+        monkeypatch.setitem(sys.modules, "hlm_attn._torch_fwd", None)  # the import raises ImportError
+        monkeypatch.delattr(hlm_attn, "_torch_fwd", raising=False)  # (an earlier import left the attribute)
+    assert _lib.torch_fwd() is None
+    assert _lib._torch_fwd is False  # remembered: no second import attempt
+    with pytest.raises(_lib.HipAttentionUnavailable, match="torch extension"):
+        _lib.load_torch_fwd()
+
+    pc = _FakePycall()
+    monkeypatch.setattr(_lib, "_pycall", pc)
+    monkeypatch.setattr(ops, "_check_inputs", lambda q, k, v: None)
+    monkeypatch.setattr(ops, "_on_index", lambda i: __import__("contextlib").nullcontext())
+    monkeypatch.setattr(ops, "_raw_stream_of", lambda i: 1234)
+    B, T, H, D = 2, 64, 4, 64
+    q = torch.zeros(B, T, H, D, dtype=torch.bfloat16)
+    k = torch.zeros(B, T, 2, D, dtype=torch.bfloat16)
+    o, lse = ops.attn_fwd_impl(q, k, k, 16, 0.125)
+    assert o.shape == (B, T, H, D) and o.dtype == torch.bfloat16
+    assert lse.shape == (B, H, T) and lse.dtype == torch.float32
+    assert len(pc.calls) == 1
+    args = pc.calls[0]
+    assert args[:5] == (q.data_ptr(), k.data_ptr(), k.data_ptr(), o.data_ptr(), lse.data_ptr())
+    assert args[6:12] == (1, B, T, H, 2, D)  # nsplit, shape
+    assert args[-3:] == (16, 0.125, 1234)  # window, scale, stream
+
+
+def test_hip_availability_requires_every_module_the_forward_needs(monkeypatch):
+    """hip_attention_available() loads the library and its CPython binding
+    (both needed by every call); a missing binding makes the backend
+    unavailable (so resolve_attention_backend can fall back) instead of
+    failing at the first forward.  The torch extension is not required."""
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.version, "hip", "7.0")
+    monkeypatch.setattr(_lib, "_torch_fwd", False)
+    assert kernels.hip_attention_available()
+
+    def missing():
+        raise _lib.HipAttentionUnavailable("no binding")
+
+    monkeypatch.setattr(_lib, "load_pycall", missing)
+    assert not kernels.hip_attention_available()
+    assert kernels.resolve_attention_backend("hip", allow_torch_backend=True) == "torch"
+
+
 def test_flop_model_matches_bench():
     import bench
 

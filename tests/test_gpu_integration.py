@@ -187,3 +187,41 @@ def test_hip_graph_capture_and_replay():
             assert torch.equal(got, want), f"replay {replay} differs from eager"
         _ = (q.float() @ k.float().transpose(-1, -2)).sum()  # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_forward_and_backward_without_the_torch_extension(monkeypatch):
+    """With the optional torch extension disabled, the forward (training
+    custom op and no-grad direct path) runs through the CPython binding of
+    the C ABI: outputs and gradients match the oracle, and both paths give
+    the same bits as with the extension."""
+    import hlm_attn
+    from hlm_attn import _lib
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(11)
+    B, T, H, D, W = 2, 333, 4, 64, 100
+    q, k, v, do = (torch.randn(B, T, H, D, generator=g).bfloat16() for _ in range(4))
+
+    def run():
+        qd, kd, vd = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+        out = hlm_attn.attention(qd, kd, vd, window_size=W)
+        out.backward(do.to(dev))
+        with torch.no_grad():
+            direct = hlm_attn.attention(qd.detach(), kd.detach(), vd.detach(), window_size=W)
+        torch.cuda.synchronize()
+        return [out.detach(), direct, qd.grad, kd.grad, vd.grad]
+
+    with_ext = run()
+    monkeypatch.setattr(_lib, "_torch_fwd", False)  # as after a failed import
+    assert _lib.torch_fwd() is None
+    without = run()
+    for a, b in zip(with_ext, without):
+        assert torch.equal(a, b)
+    ro, _ = oracle.forward(q, k, v, W)
+    rdq, rdk, rdv = oracle.backward(q, k, v, do, W)
+    for o in without[:2]:
+        err = (o.float().cpu() - ro).abs()
+        assert bool((err <= 1e-2 + 2e-2 * ro.abs()).all()), f"o max err {err.max().item():.3e}"
+    _close("dq", without[2], rdq, 3e-2)
+    _close("dk", without[3], rdk, 3e-2)
+    _close("dv", without[4], rdv, 3e-2)

@@ -190,10 +190,11 @@ BAND = 64  # queries per exact-oracle band on every (batch, head)
 @pytest.mark.parametrize("name,B,T,H,D,window,rope", FULL_CONFIGS)
 def test_full_size_slices_match_oracle(name, B, T, H, D, window, rope):
     """At BASELINE sizes, on every (batch, head) slice: the size-independent
-    invariants of tests/attn_checks.py over the whole slice, and the exact
-    oracle (o, lse, dq) on a band of 64 queries at a slice-dependent
-    position; on the first and last slice also wide bands (window + 256
-    queries) that cover every visible key of some keys, for dk and dv."""
+    invariants of tests/attn_checks.py over the whole slice, the exact
+    oracle (o, lse, dq) on a band of 64 queries and (dk, dv) on a band of 64
+    keys with every query that sees them, both at slice-dependent positions;
+    on the first and last slice also wide bands (window + 256 queries) that
+    cover every visible key of some keys, for dk and dv."""
     dev = _device()
     print(f"case {name} B={B} T={T} H={H} D={D} W={window} rope={rope}", flush=True)
     q, k, v, do = make_inputs(B, T, H, H, D, seed=11, rope=rope)
@@ -223,6 +224,24 @@ def test_full_size_slices_match_oracle(name, B, T, H, D, window, rope):
     assert_out("o", torch.stack(got["o"]), torch.stack(ref["o"]))
     assert_lse(torch.stack(got["lse"]), torch.stack(ref["lse"]))
     assert_grad("dq", torch.stack(got["dq"]), torch.stack(ref["dq"]))
+    # every slice: one 64-key band, with every query that sees those keys, so
+    # their dk / dv are complete (a row permutation or a per-slice addressing
+    # error inside a slice shows here, where the sum invariants miss it)
+    w = T if window is None else window
+    got = {"dk": [], "dv": []}
+    ref = {"dk": [], "dv": []}
+    for b in range(B):
+        for h in range(H):
+            k0 = ((b * H + h) * 613 + 5) % (T - BAND + 1)
+            q_hi = min(T, k0 + BAND + w - 1)  # the last query that sees key k0 + BAND - 1, plus one
+            sl = lambda t: t[b : b + 1, :, h : h + 1]  # noqa: E731
+            _, _, _, rdk, rdv, k_lo = oracle.band_forward_backward(sl(q), sl(k), sl(v), sl(do), window, k0, q_hi)
+            a = k0 - k_lo
+            got["dk"].append(dk[b, k0 : k0 + BAND, h]), ref["dk"].append(rdk[0, a : a + BAND, 0])
+            got["dv"].append(dv[b, k0 : k0 + BAND, h]), ref["dv"].append(rdv[0, a : a + BAND, 0])
+    print(f"  exact oracle, one {BAND}-key band (all its queries) on each of the {B * H} slices:", flush=True)
+    assert_grad("dk", torch.stack(got["dk"]), torch.stack(ref["dk"]))
+    assert_grad("dv", torch.stack(got["dv"]), torch.stack(ref["dv"]))
     # first and last slice: wide bands, dk / dv of the keys they cover completely
     w = T if window is None else window
     band = min(T, w + 256)
