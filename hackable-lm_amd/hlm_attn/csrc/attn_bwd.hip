@@ -131,6 +131,14 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   const int key_lo = max(0, q0 - W + 1);
   const int key_hi = min(T, q0 + BM) - 1;
   const int t_lo = key_lo / BN, n_tiles = key_hi / BN - t_lo + 1;
+  // Key tiles in the forward's rotated order (step t reads the tile congruent
+  // to t modulo n_tiles), so that the workgroups on one XCD, whose windows
+  // are offset by a few tiles each, read the same K/V tiles at the same step.
+  const int rot = (n_tiles - t_lo % n_tiles) % n_tiles;
+  auto tile_of = [&](int t) __attribute__((always_inline)) {
+    const int g = t + rot;
+    return t_lo + (g >= n_tiles ? g - n_tiles : g);
+  };
   int kof[CPT / NW], vof[CPT / NW];
 #pragma unroll
   for (int i = 0; i < CPT / NW; ++i) {
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   }
   // Copies tile t into the ring slot at LDS address `slot`.
   auto load_tile_at = [&](int t, unsigned slot) __attribute__((always_inline)) {
-    const int kb = (t_lo + t) * BN * sk2, vb = (t_lo + t) * BN * sv2;
+    const int kb = tile_of(t) * BN * sk2, vb = tile_of(t) * BN * sv2;
 #pragma unroll
     for (int i = 0; i < CPT / NW; ++i) {
       const unsigned piece = (unsigned)(wave + NW * i) * 1024;
@@ -238,7 +246,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
         }
       }
       const unsigned kt = (unsigned)slot * SLOTB, vt = kt + TILEB;  // constants; the base is in ab / tb
-      const int k0 = (t_lo + it) * BN;
+      const int k0 = tile_of(it) * BN;
       if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
       const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
       // All operand reads of S and dP are issued before the first MFMA.
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
         while (issued_hi < want) load_tile(++issued_hi);
       }
       const unsigned kt = (unsigned)slot * SLOTB, vt = kt + TILEB;  // constants; the base is in ab_s / atr
-      const int k0 = (t_lo + it) * BN;
+      const int k0 = tile_of(it) * BN;
       if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
       const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
       f32x16 sacc = splat16(nlse2), pacc = splat16(ndelta);
@@ -473,6 +481,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   // 2. Query tiles, visited head by head (the G query heads of this kv head),
   // tile by tile; each copy goes to ring slot (issue index) % NBUF.
   int ld_g = 0, ld_t = 0, issued = 0, islot = 0;
+  // D = 128: query tiles of each head in the rotated order (step t reads the
+  // tile congruent to t modulo nq), so that neighbouring key tiles on one XCD
+  // stream the same Q and dO rows together: 25-30% fewer L2 misses at W =
+  // 1024-2048.  At D = 64 the plain order already misses little and the
+  // rotation measured slightly slower.
+  const int rot = D == 128 ? (nq - tq_lo % nq) % nq : 0;
+  auto qtile_of = [&](int t) __attribute__((always_inline)) {
+    const int g = t + rot;
+    return g >= nq ? g - nq : g;
+  };
   const int qstep = BMQ * sq2, dostep = BMQ * sdo2;  // bytes per query tile (< 2^31: the host bounds each slab)
   const int64_t plane = (wave & 1) == 0 ? 0 : (int64_t)(a.B * H) * T;  // -lse*log2(e) or -delta rows
   // Per query head: buffer resources over its Q, dO and workspace rows from
@@ -495,14 +513,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
   }
   auto load_tile = [&]() __attribute__((always_inline)) {
     const unsigned sb = lring + (unsigned)islot * SLOTB;
-    const int tq = ld_t * qstep, tdo = ld_t * dostep;
+    const int rt = qtile_of(ld_t);
+    const int tq = rt * qstep, tdo = rt * dostep;
 #pragma unroll
     for (int i = 0; i < CPT / NW; ++i) {
       const unsigned piece = (unsigned)(wave + NW * i) * 1024;
       lds_dma_at<16>(rq, sb + piece, qof[i] + tq);
       lds_dma_at<16>(rdo, sb + TILEB + piece, dof[i] + tdo);
     }
-    lds_dma_at<4>(rst, lst + islot * 512, lane * 4 + ld_t * (BMQ * 4));  // fp32 rows, 64 lanes x 4 bytes
+    lds_dma_at<4>(rst, lst + islot * 512, lane * 4 + rt * (BMQ * 4));  // fp32 rows, 64 lanes x 4 bytes
     ++issued;
     islot = islot == NBUF - 1 ? 0 : islot + 1;
     if (++ld_t == nq) {
@@ -611,7 +630,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     const unsigned qs_t = lbase + (unsigned)slot * SLOTB, ds_t = qs_t + TILEB;
     const float* st = stbuf[slot];
-    const int qs = (tq_lo + cp_t) * BMQ;
+    const int qs = (tq_lo + qtile_of(cp_t)) * BMQ;
     if (++cp_t == nq) cp_t = 0;
     if (!(wave_live && qs <= wk_hi + W - 1 && qs + BMQ - 1 >= kw0)) continue;
     // Query rows >= T need no mask: their Q, dO and start values arrive as

@@ -14,8 +14,9 @@
 // each score block and the softmax statistics are lane-local (plus one swap
 // with lane l ^ 32).
 //
-// K/V tiles of 64 keys stream through an NBUF-slot LDS ring as whole-row
-// (coalesced) DMA in the cs layout (attn_common.h): K is read along its rows,
+// K/V tiles of 64 keys (in a rotated order, below) stream through an
+// NBUF-slot LDS ring as whole-row (coalesced) DMA in the cs layout
+// (attn_common.h): K is read along its rows,
 // V transposed with ds_read_b64_tr_b16, both without bank conflicts.  Each
 // wave's Q rows arrive the same way in a slot the ring does not use yet, and O
 // leaves through LDS as whole rows.  Key tiles outside [q0 - W + 1, q_last]
@@ -103,6 +104,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     }
   }
 
+  // Visiting order: step t reads the key tile of [t_lo, t_lo + n_tiles)
+  // that is congruent to t modulo n_tiles (a rotation of the window, not
+  // its left-to-right order).  The workgroups resident on one XCD hold
+  // neighbouring query tiles whose windows are offset by two key tiles each;
+  // left to right they would read ~64 different K/V tiles at any moment
+  // (5 MB at W = 2048, D = 128, beyond the XCD's 4 MB L2), rotated they read
+  // one or two.  Causal windows (t_lo = 0) keep the plain order.  The split
+  // forward keeps the plain order within each split's run.
+  const int rot = SPLIT ? 0 : (n_tiles - t_lo % n_tiles) % n_tiles;
+  auto tile_of = [&](int t) __attribute__((always_inline)) {
+    const int g = t + rot;
+    return t_lo + (g >= n_tiles ? g - n_tiles : g);
+  };
   // 1. This wave's Q rows into the staging area (cs layout).
 #pragma unroll
   for (int k = 0; k < NCH; ++k)
@@ -122,7 +136,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
   }
   auto load_tile = [&](int t) __attribute__((always_inline)) {
     const unsigned slot = lring + (unsigned)(t % NBUF) * SLOTB;
-    const int row0 = (t_lo + t) * BN;  // < T
+    const int row0 = tile_of(t) * BN;  // < T
     const int kskip = row0 * sk2, vskip = row0 * sv2;
     const __amdgpu_buffer_rsrc_t rk = bytes_rsrc(kslab + kskip, kext - kskip);
     const __amdgpu_buffer_rsrc_t rv = bytes_rsrc(vslab + vskip, vext - vskip);
@@ -195,7 +209,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     while (issued_hi < want) load_tile(++issued_hi);
 
     const unsigned kt = (unsigned)slot * SLOTB, vt = kt + TILEB;  // constants; lring is in ab_s / atr
-    const int k0 = (t_lo + it) * BN;
+    const int k0 = tile_of(it) * BN;
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
 
