@@ -5,7 +5,9 @@
 (kernels.py:816-841): an explicit mask is rejected, q/k/v are cast to bf16,
 the window becomes the kernels' causal look-back, the scale is 1/sqrt(D) and
 the result is bf16 in (B, T, H, D).  Like the FlashAttention-3/4 branches
-(kernels.py:842-843) it rejects dropout.
+(kernels.py:842-843) it rejects dropout.  backend="torch" is the reference's
+dense math on (B, H, T, D) tensors (kernels.py:785-800), which the mirrored
+AttentionCore runs for CPU tensors as the reference's does (model.py:170).
 
 `hip_attention_available` and `resolve_attention_backend` mirror the probe and
 fallback rules of resolve_kernel_backends (kernels.py:146-242) for the
@@ -140,11 +142,14 @@ def scaled_dot_product_attention(
     window_size: int | None = None,
     backend: str = HIP_BACKEND,
 ) -> torch.Tensor:
-    """Dispatch entry with the reference's signature; implements backend="hip"."""
+    """Dispatch entry with the reference's signature; implements backend="hip"
+    and the reference's backend="torch" math."""
+    if backend == "torch":
+        return _torch_sdpa(q, k, v, dropout_p, is_causal, attn_mask)
     if backend != HIP_BACKEND:
         raise RuntimeError(
-            f"unsupported attention backend {backend!r}: this library implements only {HIP_BACKEND!r}; "
-            "the other backends stay in the host model's kernels.py"
+            f"unsupported attention backend {backend!r}: this library implements only {HIP_BACKEND!r} "
+            "and the reference's 'torch' math; the other backends stay in the host model's kernels.py"
         )
     if attn_mask is not None or block_mask is not None:
         raise RuntimeError(f"{backend} path expects window_size instead of an explicit attention mask")
@@ -153,6 +158,35 @@ def scaled_dot_product_attention(
     if not is_causal:
         raise RuntimeError(f"{backend} backend implements causal attention only")
     return attention(q, k, v, window_size=window_size)
+
+
+def _torch_sdpa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dropout_p: float,
+    is_causal: bool,
+    attn_mask: torch.Tensor | None,
+) -> torch.Tensor:
+    """The reference's backend="torch" (kernels.py:785-800) on (B, H, T, D):
+    scores q.k^T / sqrt(D) in the inputs' dtype, the causal triangle and a bool
+    mask filled with -inf (a float mask is added), softmax in fp32 cast back,
+    optional dropout, then P @ v.  Plain torch operators on any device; the
+    transposed k is made contiguous before the product."""
+    scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(q.shape[-1]))
+    if is_causal:
+        n_q, n_k = scores.shape[-2], scores.shape[-1]
+        keep = torch.ones((n_q, n_k), dtype=torch.bool, device=q.device).tril()
+        scores = scores.masked_fill(~keep, float("-inf"))
+    if attn_mask is not None:
+        if attn_mask.dtype == torch.bool:
+            scores = scores.masked_fill(~attn_mask, float("-inf"))
+        else:
+            scores = scores + attn_mask
+    probs = torch.softmax(scores.float(), dim=-1).to(dtype=q.dtype)
+    if dropout_p:
+        probs = torch.nn.functional.dropout(probs, p=dropout_p, training=True)
+    return torch.matmul(probs, v)
 
 
 def qk_norm_rope_hip(

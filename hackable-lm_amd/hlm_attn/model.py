@@ -13,8 +13,11 @@ QKVProjection mirrors model.py:76-126: the fused q/k/v projection, then the
 q/k RMSNorm + partial RoPE producer; `fwd_hip` is `fwd_triton` with the HIP
 producer in place of the Triton one, fed the same views and rotary tables.
 
-The reference routes CPU tensors to its own `torch` backend
-(model.py:170); this library has no CPU path and raises instead.
+AttentionCore routes CPU tensors to `fwd_torch`, the reference's dense math
+(model.py:170, :176-196 with kernels.py:785-800), as the reference does;
+attention_backend="torch" selects it on any device.  The hip backend never
+falls back to it: a ROCm tensor without libhlm_attn.so raises.  The other
+modules have no CPU path and raise on CPU tensors.
 """
 from __future__ import annotations
 
@@ -135,12 +138,29 @@ class AttentionCore(nn.Module):
             layer_idx, config.n_layer, config.attention_window, config.attention_full_every
         )
         self.dropout = config.dropout
+        self._mask_cache: torch.Tensor | None = None
 
     def _attention_window_size(self, seq_len: int) -> int | None:
         return attention_window_size(self.attention_window, seq_len)
 
+    def _sliding_window_mask(self, seq_len: int, device: torch.device) -> torch.Tensor | None:
+        """model.py:141-151: bool (1, 1, T, T), True where 0 <= i - j < window,
+        None when the layer has no window or it covers the sequence; kept for
+        the last (T, device)."""
+        if self._attention_window_size(seq_len) is None:
+            return None
+        cached = self._mask_cache
+        if cached is None or cached.shape[-1] != seq_len or cached.device != device:
+            pos = torch.arange(seq_len, device=device)
+            lag = pos[:, None] - pos[None, :]
+            cached = ((lag >= 0) & (lag < self.attention_window))[None, None]
+            self._mask_cache = cached
+        return cached
+
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         backend = normalize_attention_backend(self.config.attention_backend)
+        if q.device.type == "cpu":  # model.py:170
+            backend = "torch"
         fwd_backend = getattr(self, f"fwd_{backend}", None)
         if fwd_backend is None:
             raise RuntimeError(f"{type(self).__name__} does not support backend {backend!r}")
@@ -157,6 +177,29 @@ class AttentionCore(nn.Module):
             window_size=self._attention_window_size(q.shape[1]),
             backend="hip",
         )
+
+    def fwd_torch(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """model.py:176-196: heads first, k/v heads repeated for GQA, the window
+        as an explicit mask (plain causal without one), the reference's dense
+        math, (B, T, H, D) back."""
+        seq_len = q.shape[1]
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        if self.n_kv_head != self.n_head:
+            group = self.n_head // self.n_kv_head
+            k = k.repeat_interleave(group, dim=1)
+            v = v.repeat_interleave(group, dim=1)
+        mask = self._sliding_window_mask(seq_len, q.device)
+        y = kernels.scaled_dot_product_attention(
+            q,
+            k,
+            v,
+            self.dropout if self.training else 0.0,
+            is_causal=mask is None,
+            attn_mask=mask,
+            window_size=self._attention_window_size(seq_len),
+            backend="torch",
+        )
+        return y.transpose(1, 2)
 
 
 class LMHeadProjection(nn.Module):

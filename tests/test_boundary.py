@@ -291,18 +291,19 @@ def test_attention_core_uses_layer_pattern(fake_op):
     cores = [model.AttentionCore(cfg, i) for i in range(8)]
     assert [c.attention_window for c in cores] == [4, 4, 4, None, 4, 4, 4, None]
     q = torch.randn(1, 8, 2, 64)
-    out = cores[0](q, q, q)
+    # CPU tensors take the torch math (model.py:170), so the hip method is called directly here
+    out = cores[0].fwd_hip(q, q, q)
     assert out.shape == q.shape and out.dtype == torch.bfloat16
     assert fake_op.calls[-1][5] == 4
-    cores[3](q, q, q)
+    cores[3].fwd_hip(q, q, q)
     assert fake_op.calls[-1][5] == 0
     # W >= T is plain causal (model.py:155-159)
-    cores[0](q[:, :4], q[:, :4], q[:, :4])
+    cores[0].fwd_hip(q[:, :4], q[:, :4], q[:, :4])
     assert fake_op.calls[-1][5] == 0
     cores[0].train()
     cores[0].dropout = 0.1
     with pytest.raises(RuntimeError, match="dropout"):
-        cores[0](q, q, q)
+        cores[0].fwd_hip(q, q, q)
 
 
 def test_attention_core_rejects_unknown_backend():
@@ -310,9 +311,75 @@ def test_attention_core_rejects_unknown_backend():
     core = model.AttentionCore(cfg, 0)
     with pytest.raises(ValueError, match="unknown attention_backend"):
         core(torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64))
+    # a known backend this library does not carry; meta tensors are not routed to the CPU math
     cfg2 = model.AttentionConfig(n_layer=2, n_head=2, n_kv_head=2, attention_backend="flash_attn_2")
+    meta = torch.zeros(1, 4, 2, 64, device="meta")
     with pytest.raises(RuntimeError, match="does not support backend"):
-        model.AttentionCore(cfg2, 0)(torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64), torch.zeros(1, 4, 2, 64))
+        model.AttentionCore(cfg2, 0)(meta, meta, meta)
+
+
+@pytest.mark.parametrize("backend", ["hip", "torch", "flash_attn_2"])
+def test_attention_core_routes_cpu_tensors_to_the_torch_math(fake_op, backend):
+    """model.py:169-196: CPU tensors take fwd_torch whatever the configured
+    backend; every layer of the 8-layer pattern, with GQA, in fp32 and bf16,
+    matches the oracle's restatement of that path (pinned by test_oracle
+    against the reference's closed-form test and brute force) and the
+    fp64 brute-force loops; the HIP op is never called."""
+    cfg = model.AttentionConfig(n_layer=8, n_head=4, n_kv_head=2, attention_window=5,
+                                attention_full_every=4, attention_backend=backend)
+    gen = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(2, 9, h, 16, generator=gen) for h in (4, 2, 2))
+    for layer in (0, 3, 7):
+        core = model.AttentionCore(cfg, layer).eval()
+        window = None if layer in (3, 7) else 5
+        out = core(q, k, v)
+        assert out.shape == q.shape and out.dtype == torch.float32
+        assert torch.equal(out, oracle.attention_core_torch(q, k, v, window))
+        brute, _ = oracle.brute_force_forward(q.double().numpy(), k.double().numpy(), v.double().numpy(), window)
+        assert torch.allclose(out.double(), torch.from_numpy(brute), atol=1e-5)
+        ob = core(q.bfloat16(), k.bfloat16(), v.bfloat16())
+        assert ob.dtype == torch.bfloat16
+        assert torch.equal(ob, oracle.attention_core_torch(q.bfloat16(), k.bfloat16(), v.bfloat16(), window))
+    assert fake_op.calls == []
+
+
+def test_attention_core_torch_path_mask_cache_and_dropout():
+    """The window mask is built once per sequence length (model.py:141-151);
+    training-mode dropout is applied to the probabilities (kernels.py:798-799),
+    so p = 1 zeroes the output, and eval mode applies none."""
+    cfg = model.AttentionConfig(n_layer=4, n_head=2, n_kv_head=2, attention_window=3, attention_backend="torch")
+    core = model.AttentionCore(cfg, 0)
+    q = torch.randn(1, 7, 2, 8)
+    m1 = core._sliding_window_mask(7, q.device)
+    assert core._sliding_window_mask(7, q.device) is m1
+    assert torch.equal(m1[0, 0], oracle.sliding_window_mask(7, 3)[0, 0])
+    assert core._sliding_window_mask(6, q.device).shape == (1, 1, 6, 6)
+    assert core._sliding_window_mask(3, q.device) is None  # W >= T: plain causal
+    core.dropout = 1.0
+    core.train()
+    assert torch.equal(core(q, q, q), torch.zeros_like(q))
+    core.eval()
+    assert torch.equal(core(q, q, q), oracle.attention_core_torch(q, q, q, 3))
+
+
+def test_sdpa_torch_branch_matches_reference_closed_form_test(fake_op):
+    """kernels.py:785-800 through the dispatcher, on the reference's
+    tests/test_kernels.py:97-130 case (B2 H3 T5, Dqk=7, Dv=9, causal and
+    distance < 3, (B, H, T, D)) against softmax(QK^T/sqrt(d) masked) V; an
+    additive float mask of 0 / -inf gives the same result as the bool mask."""
+    gen = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(2, 3, 5, d, generator=gen, dtype=torch.float64) for d in (7, 7, 9))
+    lag = torch.arange(5)[:, None] - torch.arange(5)[None, :]
+    mask = ((lag >= 0) & (lag < 3))[None, None]
+    ref = torch.softmax((q @ k.transpose(-2, -1) / math.sqrt(7)).masked_fill(~mask, float("-inf")), dim=-1) @ v
+    out = kernels.scaled_dot_product_attention(q.float(), k.float(), v.float(), 0.0, is_causal=False,
+                                               attn_mask=mask, backend="torch")
+    assert torch.allclose(out.double(), ref, atol=1e-6)  # the reference test's own tolerance
+    additive = torch.zeros(5, 5).masked_fill(~mask[0, 0], float("-inf"))
+    out_add = kernels.scaled_dot_product_attention(q.float(), k.float(), v.float(), 0.0, is_causal=True,
+                                                   attn_mask=additive, backend="torch")
+    assert torch.equal(out_add, out)
+    assert fake_op.calls == []
 
 
 # --- config mirror -----------------------------------------------------------------
