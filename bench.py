@@ -146,6 +146,18 @@ class Problem:
     def bwd(self):
         self._bwd(self.lib.hlm_attn_bwd)
 
+    def bwd_fused(self, part, nbytes: int):
+        """The single-pass backward (hlm_attn_bwd_fused, D = 64) into the same
+        outputs, with `part` (nbytes) as its partial workspace."""
+        rc = self.lib.hlm_attn_bwd_fused(
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(),
+            self.lse.data_ptr(), self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.delta.data_ptr(),
+            part.data_ptr(), nbytes,
+            *self.dims, self.s["q"], self.s["k"], self.s["v"], self.s["o"], self.s["do"], self.s["dq"],
+            self.s["dk"], self.s["dv"], self.window, self.scale, self.stream,
+        )
+        assert rc == 0, self.lib.hlm_attn_last_error()
+
     def bwd_dq(self):
         self._bwd(self.lib.hlm_attn_bwd_dq)
 
@@ -605,6 +617,52 @@ def measure(name: str, steps: int, warmup: int, device, graph: bool = False, ker
     }
 
 
+def measure_bwd_fused(names, reps: int, device, rounds: int = 5) -> dict:
+    """The single-pass backward (hlm_attn_bwd_fused: delta rows, one
+    key-stationary pass writing dK, dV and bf16 dQ partials, a reduce of the
+    partials) beside the two-kernel backward (hlm_attn_bwd), on the same
+    inputs and forward outputs, for the D = 64 configs `names`.  Each path:
+    `reps` back-to-back launches timed by HIP events, `rounds` alternating
+    rounds, the minimum reported; the results of the two paths compared."""
+    import torch
+
+    out = {"timing": f"min over {rounds} alternating rounds of HIP events around {reps} back-to-back launches",
+           "configs": {}}
+    for name in names:
+        cfg = CONFIGS[name]
+        prob = Problem(cfg, seed=0, device=device)
+        prob.fwd()
+        B, T, H, _, D = prob.dims
+        nbytes = prob.lib.hlm_attn_bwd_fused_workspace_bytes(B, T, H, D, prob.window)
+        assert nbytes > 0, prob.lib.hlm_attn_last_error()
+        part = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        fused = lambda: prob.bwd_fused(part, nbytes)  # noqa: E731
+        prob.bwd()
+        two = [t.clone() for t in (prob.dq, prob.dk, prob.dv)]
+        fused()
+        torch.cuda.synchronize()
+        dq_rel = ((prob.dq.float() - two[0].float()).norm() / two[0].float().norm()).item()
+        same_dk_dv = bool(torch.equal(prob.dk, two[1]) and torch.equal(prob.dv, two[2]))
+        prewarm(torch, prob.bwd, min_ms=50.0)
+        times = {"two_kernel": [], "single_pass": []}
+        for _ in range(rounds):
+            times["two_kernel"].append(event_time_ms(torch, prob.bwd, reps))
+            times["single_pass"].append(event_time_ms(torch, fused, reps))
+        best = {k: min(v) * 1e3 for k, v in times.items()}
+        fl = effective_flops(cfg)["bwd"]
+        out["configs"][name] = {
+            "bwd_us": {k: round(v, 2) for k, v in best.items()},
+            "bwd_tflops": {k: round(fl / (v * 1e-6) / 1e12, 1) for k, v in best.items()},
+            "single_pass_over_two_kernel": round(best["single_pass"] / best["two_kernel"], 3),
+            "partial_workspace_MB": round(nbytes / 1e6, 1),
+            "dk_dv_bit_identical": same_dk_dv,
+            "dq_norm_rel_vs_two_kernel": float(f"{dq_rel:.3e}"),
+        }
+        del prob, part, two
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # The other BASELINE configs, measured in the same run ("configs" object).
 # ---------------------------------------------------------------------------
@@ -854,6 +912,9 @@ def main() -> int:
     ap.add_argument("--no-producer", action="store_true", help="skip the q/k RMSNorm + RoPE producer's timing")
     ap.add_argument("--no-eval", action="store_true", help="skip the evaluation-path (no-grad, batch 1) timings")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the LM-head cross-entropy timing")
+    ap.add_argument("--bwd-fused", nargs="?", const="cfg2_local,cfg3_full", default=None, metavar="CONFIGS",
+                    help="also time the single-pass backward (hlm_attn_bwd_fused) against the two-kernel one at "
+                    "these comma-separated D = 64 configs (default cfg2_local,cfg3_full; object bwd_fused)")
     ap.add_argument(
         "--copy-mib", type=int, default=0,
         help="after timing, run one device-to-device copy of this many MiB: a kernel of known "
@@ -934,6 +995,13 @@ def main() -> int:
     if not args.no_lm_head:
         line["lm_head"] = measure_lm_head(max(args.steps // 4, 20), 5, device)
         line["residual_norm"] = measure_residual_norm(max(args.steps // 2, 50), 10, device)
+    if args.bwd_fused:
+        names = [n for n in args.bwd_fused.split(",") if n]
+        bad = [n for n in names if n not in CONFIGS or CONFIGS[n]["D"] != 64]
+        if bad:
+            print(f"--bwd-fused takes D = 64 configs only, not {bad}", file=sys.stderr)
+            return 2
+        line["bwd_fused"] = measure_bwd_fused(names, max(args.steps, 50), device)
     if not args.no_cpu_baseline:
         # last: ~10 s of host work, after which the GPU has idled and would need a new pre-warm
         line["cpu_baseline"] = cpu_baseline()

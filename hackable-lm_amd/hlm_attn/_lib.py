@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libhlm_attn.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Every symbol include/hlm_attn.h declares, with its (restype, argtypes).
 _P = ctypes.c_void_p
@@ -25,6 +25,9 @@ _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _S,
 for _name in ("hlm_attn_bwd", "hlm_attn_bwd_dq", "hlm_attn_bwd_dkdv"):
     SIGNATURES[_name] = (_I, _BWD_ARGTYPES)
 SIGNATURES["hlm_attn_bwd_noalloc"] = (_I, _BWD_ARGTYPES[:9] + _BWD_ARGTYPES[10:])  # no delta_ws
+# the single-pass backward: + partial workspace (pointer, bytes) after delta_ws
+SIGNATURES["hlm_attn_bwd_fused"] = (_I, _BWD_ARGTYPES[:10] + [_P, ctypes.c_int64] + _BWD_ARGTYPES[10:])
+SIGNATURES["hlm_attn_bwd_fused_workspace_bytes"] = (ctypes.c_int64, [_I, _I, _I, _I, _I])
 SIGNATURES["hlm_attn_fwd_split"] = (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _S, _S, _I, _F, _P])
 SIGNATURES["hlm_attn_fwd_split_count"] = (_I, [_I, _I, _I, _I, _I])
 SIGNATURES["hlm_qk_norm_rope_fwd"] = (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _S, _S, _F, _P])

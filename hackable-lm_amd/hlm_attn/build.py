@@ -19,7 +19,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libhlm_attn.so"
-SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
+SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_bwd_fused.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
 ARCH = "gfx950"
 PYCALL_PATH = PKG_DIR / ("_pycall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 TORCH_FWD_PATH = PKG_DIR / "_torch_fwd.so"
@@ -42,6 +42,7 @@ HIPCC_FLAGS = [
 PER_SOURCE_FLAGS = {
     "attn_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "attn_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "attn_bwd_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
 

@@ -16,6 +16,8 @@ template <int D>
 int fwd_split_count(int B, int T, int H, int W);
 template <int D>
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream, int phases);
+int fused_partial_slots(int T, int W);
+hipError_t launch_bwd_fused(const BwdArgs& a, bf16* part, int R, hipStream_t stream);
 template <int D>
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, bool backward, hipStream_t stream);
 hipError_t launch_ce_rows(void* logits, bool bf16_logits, int64_t row_stride, const int64_t* targets, float* loss,
@@ -79,7 +81,7 @@ void copy3(int64_t dst[3], const int64_t* src) {
 
 extern "C" {
 
-int hlm_attn_abi_version(void) { return 7; }
+int hlm_attn_abi_version(void) { return 8; }
 
 const char* hlm_attn_last_error(void) { return g_last_error; }
 
@@ -175,15 +177,32 @@ int check_bwd(const void* q, const void* k, const void* v, const void* o, const 
   return HLM_ATTN_OK;
 }
 
+// phases: kBwdDq / kBwdDkDv / kBwdAll for the two-kernel backward, or
+// kBwdFused (with `part`, `part_bytes`) for the single-pass one.
+constexpr int kBwdFused = 4;
+
 int run_bwd(int phases, const void* q, const void* k, const void* v, const void* o, const void* dout,
             const float* lse, void* dq, void* dk, void* dv, float* delta_ws, int B, int T, int H, int Hkv,
             int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
             const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
-            const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale, void* stream) {
+            const int64_t* dk_strides, const int64_t* dv_strides, int window, float scale, void* stream,
+            void* part = nullptr, int64_t part_bytes = 0) {
   g_last_error[0] = '\0';
   int rc = check_bwd(q, k, v, o, dout, lse, dq, dk, dv, B, T, H, Hkv, D, q_strides, k_strides, v_strides, o_strides,
                      do_strides, dq_strides, dk_strides, dv_strides, scale);
-  if (rc || B == 0 || T == 0) return rc;
+  if (rc) return rc;
+  int R = 0;
+  if (phases == kBwdFused) {
+    if (D != 64) return fail(HLM_ATTN_EUNSUPPORTED, "the single-pass backward takes head_dim 64 only (got %d)", D);
+    if (B == 0 || T == 0) return HLM_ATTN_OK;
+    R = hlm::fused_partial_slots(T, effective_window(window, T));
+    const int64_t need = (int64_t)R * B * H * T * D * 2;
+    if (part == nullptr || !aligned16(part)) return fail(HLM_ATTN_EINVAL, "partial workspace is null or not 16-byte aligned");
+    if (part_bytes < need)
+      return fail(HLM_ATTN_EINVAL, "partial workspace holds %lld bytes, %lld needed", (long long)part_bytes,
+                  (long long)need);
+  }
+  if (B == 0 || T == 0) return rc;
   if (delta_ws == nullptr) return fail(HLM_ATTN_EINVAL, "delta_ws is a null pointer");
   hlm::BwdArgs a;
   a.q = static_cast<const hlm::bf16*>(q);
@@ -212,7 +231,9 @@ int run_bwd(int phases, const void* q, const void* k, const void* v, const void*
   a.scale = scale;
   a.scale_log2 = scale * hlm::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t err = D == 64 ? hlm::launch_bwd<64>(a, s, phases) : hlm::launch_bwd<128>(a, s, phases);
+  const hipError_t err = phases == kBwdFused ? hlm::launch_bwd_fused(a, static_cast<hlm::bf16*>(part), R, s)
+                         : D == 64           ? hlm::launch_bwd<64>(a, s, phases)
+                                             : hlm::launch_bwd<128>(a, s, phases);
   if (err != hipSuccess) return fail(HLM_ATTN_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
   return HLM_ATTN_OK;
 }
@@ -317,6 +338,25 @@ extern "C" {
 int hlm_attn_bwd(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdAll, HLM_BWD_ARGS); }
 int hlm_attn_bwd_dq(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDq, HLM_BWD_ARGS); }
 int hlm_attn_bwd_dkdv(HLM_BWD_PARAMS) { return run_bwd(hlm::kBwdDkDv, HLM_BWD_ARGS); }
+
+int64_t hlm_attn_bwd_fused_workspace_bytes(int B, int T, int H, int D, int window) {
+  g_last_error[0] = '\0';
+  if (B < 0 || T < 0 || H <= 0) return fail(HLM_ATTN_EINVAL, "bad shape B=%d T=%d H=%d", B, T, H);
+  if (D != 64) return fail(HLM_ATTN_EUNSUPPORTED, "the single-pass backward takes head_dim 64 only (got %d)", D);
+  if (B == 0 || T == 0) return 0;
+  return (int64_t)hlm::fused_partial_slots(T, effective_window(window, T)) * B * H * T * D * 2;
+}
+
+int hlm_attn_bwd_fused(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                       const float* lse, void* dq, void* dk, void* dv, float* delta_ws, void* partial_ws,
+                       int64_t partial_ws_bytes, int B, int T, int H, int Hkv, int D, const int64_t* q_strides,
+                       const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                       const int64_t* do_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                       const int64_t* dv_strides, int window, float scale, void* stream) {
+  return run_bwd(kBwdFused, q, k, v, o, dout, lse, dq, dk, dv, delta_ws, B, T, H, Hkv, D, q_strides, k_strides,
+                 v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides, window, scale, stream,
+                 partial_ws, partial_ws_bytes);
+}
 
 }  // extern "C"
 

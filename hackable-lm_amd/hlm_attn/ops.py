@@ -9,11 +9,16 @@ implementations only describe shapes, and the real ones allocate through
 torch's caching allocator, launch on torch's current stream and never
 synchronise.  There is no CPU implementation: on a tensor that is not on a
 ROCm device, or without libhlm_attn.so, the ops raise.
+
+The backward runs the two-kernel path (hlm_attn_bwd: dq, then dkdv) unless
+HLM_ATTN_BWD=fused selects the single-pass one (hlm_attn_bwd_fused, head
+dim 64 only; other head dims keep the two-kernel path).
 """
 from __future__ import annotations
 
 import contextlib
 import ctypes
+import os
 
 import torch
 
@@ -207,17 +212,32 @@ def hip_attn_bwd(
     dk = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     dv = torch.empty((B, T, Hkv, D), dtype=_BF16, device=q.device)
     delta = torch.empty((2, B, H, T), dtype=torch.float32, device=q.device)  # -lse*log2(e), -rowsum(dO*O)
+    strides = (_lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o),
+               _lib.strides3(dout), _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv))
     with _on_device(q.device):
-        rc = lib.hlm_attn_bwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),
-            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
-            B, T, H, Hkv, D,
-            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(o),
-            _lib.strides3(dout), _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv),
-            int(window), float(scale), _stream_handle(q.device),
-        )
+        if D == 64 and fused_backward_selected():
+            nbytes = lib.hlm_attn_bwd_fused_workspace_bytes(B, T, H, D, int(window))
+            if nbytes < 0:
+                _lib.check(int(nbytes), lib)
+            part = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=q.device)
+            rc = lib.hlm_attn_bwd_fused(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), part.data_ptr(), int(nbytes),
+                B, T, H, Hkv, D, *strides, int(window), float(scale), _stream_handle(q.device),
+            )
+        else:
+            rc = lib.hlm_attn_bwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(),
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+                B, T, H, Hkv, D, *strides, int(window), float(scale), _stream_handle(q.device),
+            )
     _lib.check(rc, lib)
     return dq, dk, dv
+
+
+def fused_backward_selected() -> bool:
+    """True when HLM_ATTN_BWD=fused asks for the single-pass backward."""
+    return os.environ.get("HLM_ATTN_BWD", "").lower() == "fused"
 
 
 @hip_attn_bwd.register_fake

@@ -144,6 +144,34 @@ int hlm_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* o
                       int window, float scale, void* stream);
 
 /*
+ * Single-pass backward (head_dim 64 only): the same gradients as
+ * hlm_attn_bwd, with S and dP formed once per score block.  Three kernels
+ * on `stream`: the delta workspace rows; one key-stationary pass that
+ * writes dk, dv and per-key-tile dQ partials (bf16) into partial_ws; and a
+ * reduce of the partials into dq.  dk and dv are bit-identical to
+ * hlm_attn_bwd's; dq differs by the rounding of the partials.  partial_ws
+ * (16-byte aligned) must hold hlm_attn_bwd_fused_workspace_bytes(B, T, H, D,
+ * window) bytes, passed as partial_ws_bytes; other arguments as for
+ * hlm_attn_bwd.  D != 64 returns HLM_ATTN_EUNSUPPORTED.  Replaces the same
+ * call as hlm_attn_bwd (FlashAttention-2's backward behind
+ * /root/reference/kernels.py:841); an alternative implementation of it,
+ * selected by the caller.
+ */
+int hlm_attn_bwd_fused(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                       const float* lse, void* dq, void* dk, void* dv, float* delta_ws,
+                       void* partial_ws, int64_t partial_ws_bytes,
+                       int B, int T, int H, int Hkv, int D,
+                       const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                       const int64_t* o_strides, const int64_t* do_strides, const int64_t* dq_strides,
+                       const int64_t* dk_strides, const int64_t* dv_strides,
+                       int window, float scale, void* stream);
+/* Bytes of hlm_attn_bwd_fused's partial workspace: R * B * H * T * D * 2 with
+ * R the most 128-key tiles one 32-row query tile meets (ceil((W - 1) / 128)
+ * + 1 or fewer; ceil(T / 128) for plain causal).  Negative: an HLM_ATTN_E*
+ * code (D != 64, bad shape). */
+int64_t hlm_attn_bwd_fused_workspace_bytes(int B, int T, int H, int D, int window);
+
+/*
  * hlm_attn_bwd without the caller's workspace: the same computation and
  * results as hlm_attn_bwd (bit for bit), with the workspace held in a
  * fixed device array inside the library, so the call allocates nothing

@@ -134,6 +134,57 @@ def test_bwd_phases_validate_like_bwd():
         assert rc == -2
 
 
+def _partials_per_row_bound(T: int, W: int) -> int:
+    """The most 128-key tiles that any query row's keys (q - W + 1 .. q) meet."""
+    W = T if W <= 0 or W >= T else W
+    return max(q // 128 - max(0, q - W + 1) // 128 + 1 for q in range(T))
+
+
+@pytest.mark.parametrize("B,T,H,W", [(8, 2048, 12, 512), (8, 2048, 12, 0), (1, 640, 2, 513), (2, 37, 3, 5),
+                                     (1, 1, 2, 0), (1, 700, 2, 129)])
+def test_fused_backward_workspace_covers_every_partial(B, T, H, W):
+    """hlm_attn_bwd_fused_workspace_bytes: one bf16 (B, H, T, 64) plane per
+    128-key tile that a row can meet -- W = 512 gives 5, plain causal T / 128."""
+    lib = _lib.load()
+    R = _partials_per_row_bound(T, W)
+    assert lib.hlm_attn_bwd_fused_workspace_bytes(B, T, H, 64, W) == R * B * H * T * 64 * 2
+    if (T, W) == (2048, 512):
+        assert R == 5
+    if W == 0:
+        assert R == (T + 127) // 128
+
+
+def test_fused_backward_validates_before_touching_the_device():
+    lib = _lib.load()
+    s = _strides(2048, 128, 64)
+    p = ctypes.c_void_p(0x1000)
+    fn = lib.hlm_attn_bwd_fused
+    need = lib.hlm_attn_bwd_fused_workspace_bytes(1, 16, 2, 64, 0)
+    assert need == 1 * 1 * 2 * 16 * 64 * 2
+    # head dim 128: not implemented by the single pass
+    rc = fn(p, p, p, p, p, p, p, p, p, p, p, 1 << 30, 1, 16, 2, 2, 128, s, s, s, s, s, s, s, s, 0, 0.125, None)
+    assert rc == -2 and b"head_dim 64 only" in lib.hlm_attn_last_error()
+    assert lib.hlm_attn_bwd_fused_workspace_bytes(1, 16, 2, 128, 0) == -2
+    # a workspace one byte short, or none
+    rc = fn(p, p, p, p, p, p, p, p, p, p, p, need - 1, 1, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None)
+    assert rc == -1 and b"needed" in lib.hlm_attn_last_error()
+    rc = fn(p, p, p, p, p, p, p, p, p, p, None, need, 1, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None)
+    assert rc == -1 and b"partial workspace" in lib.hlm_attn_last_error()
+    # the shared argument checks of hlm_attn_bwd come first
+    rc = fn(p, p, p, p, p, None, p, p, p, p, p, need, 1, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None)
+    assert rc == -1 and b"lse" in lib.hlm_attn_last_error()
+    assert fn(p, p, p, p, p, p, p, p, p, p, None, 0, 0, 16, 2, 2, 64, s, s, s, s, s, s, s, s, 0, 0.125, None) == 0
+
+
+def test_fused_backward_switch_is_off_by_default(monkeypatch):
+    monkeypatch.delenv("HLM_ATTN_BWD", raising=False)
+    assert not ops.fused_backward_selected()
+    monkeypatch.setenv("HLM_ATTN_BWD", "Fused")
+    assert ops.fused_backward_selected()
+    monkeypatch.setenv("HLM_ATTN_BWD", "two-kernel")
+    assert not ops.fused_backward_selected()
+
+
 def test_noalloc_backward_validates_and_bounds_its_scratch_before_touching_the_device():
     """hlm_attn_bwd_noalloc: argument errors like hlm_attn_bwd's, and problems
     beyond its fixed scratch (B * H * T > 4,194,304 query rows) rejected with
