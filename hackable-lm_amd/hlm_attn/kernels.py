@@ -172,7 +172,8 @@ def _torch_sdpa(
     scores q.k^T / sqrt(D) in the inputs' dtype, the causal triangle and a bool
     mask filled with -inf (a float mask is added), softmax in fp32 cast back,
     optional dropout, then P @ v.  Plain torch operators on any device; the
-    transposed k is made contiguous before the product."""
+    right operand of each product (k transposed, v) is made contiguous first,
+    since bf16 batched products on ROCm have faulted on strided right operands."""
     scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(q.shape[-1]))
     if is_causal:
         n_q, n_k = scores.shape[-2], scores.shape[-1]
@@ -186,7 +187,7 @@ def _torch_sdpa(
     probs = torch.softmax(scores.float(), dim=-1).to(dtype=q.dtype)
     if dropout_p:
         probs = torch.nn.functional.dropout(probs, p=dropout_p, training=True)
-    return torch.matmul(probs, v)
+    return torch.matmul(probs, v.contiguous())
 
 
 def qk_norm_rope_hip(

@@ -97,6 +97,34 @@ def test_autograd_through_attention_core_layers():
         _close("dv", vd.grad, rdv, 3e-2)
 
 
+def test_attention_core_backend_switch_on_the_gpu():
+    """The drop-in as a model sees it: one AttentionCore, attention_backend
+    flipped from the reference's "torch" math (fp32 on the GPU here, so no
+    bf16 batched product runs) to "hip", on the same ROCm tensors; outputs
+    and gradients agree within the parity tolerances, GQA and a window."""
+    from hlm_attn import AttentionConfig, AttentionCore
+
+    dev = _dev()
+    B, T, H, Hkv, D = 2, 300, 4, 2, 64
+    g = torch.Generator().manual_seed(21)
+    q, k, v, do = (torch.randn(B, T, h, D, generator=g).bfloat16() for h in (H, Hkv, Hkv, H))
+    grads = {}
+    for backend in ("torch", "hip"):
+        cfg = AttentionConfig(n_layer=4, n_head=H, n_kv_head=Hkv, attention_window=100, attention_backend=backend)
+        core = AttentionCore(cfg, 0).eval()
+        dtype = torch.float32 if backend == "torch" else torch.bfloat16
+        qd, kd, vd = (t.to(dev, dtype).requires_grad_(True) for t in (q, k, v))
+        out = core(qd, kd, vd)
+        out.backward(do.to(dev, dtype))
+        torch.cuda.synchronize()
+        grads[backend] = [t.detach().float().cpu() for t in (out, qd.grad, kd.grad, vd.grad)]
+    ref, got = grads["torch"], grads["hip"]
+    err = (got[0] - ref[0]).abs()
+    assert bool((err <= 1e-2 + 2e-2 * ref[0].abs()).all())
+    for name, a, b in zip(("dq", "dk", "dv"), got[1:], ref[1:]):
+        _close(name, a, b, 3e-2)
+
+
 def test_expanded_upstream_gradient():
     """o.sum().backward() hands the backward an expanded dO (all strides 0)."""
     import hlm_attn
