@@ -124,3 +124,35 @@ def test_fused_backward_through_autograd(monkeypatch):
     assert_grad("dq", qd.grad.float().cpu(), rdq)
     assert_grad("dk", kd.grad.float().cpu(), rdk)
     assert_grad("dv", vd.grad.float().cpu(), rdv)
+
+
+def test_fused_backward_with_strided_views_and_expanded_grad(monkeypatch):
+    """Strides the model hands the backward: q, k, v as views of one fused
+    projection (row stride 3 H D) and an expanded upstream gradient
+    (o.sum().backward(): all strides 0); the switch changes dK/dV by nothing
+    and dQ by the rounding of its partials."""
+    import hlm_attn
+
+    dev = _device()
+    B, T, H, D = 2, 260, 4, 64
+    g = torch.Generator().manual_seed(31)
+    fused = torch.randn(B, T, 3 * H * D, generator=g).bfloat16().to(dev)
+    grads = {}
+    for mode in ("two", "fused"):
+        if mode == "fused":
+            monkeypatch.setenv("HLM_ATTN_BWD", "fused")
+        else:
+            monkeypatch.delenv("HLM_ATTN_BWD", raising=False)
+        leaf = fused.clone().requires_grad_(True)
+        q, k, v = (t.view(B, T, H, D) for t in leaf.split((H * D, H * D, H * D), dim=-1))
+        assert not v.is_contiguous()
+        hlm_attn.attention(q, k, v, window_size=70).float().sum().backward()
+        torch.cuda.synchronize()
+        grads[mode] = leaf.grad.view(B, T, 3, H, D)
+    two, one = grads["two"], grads["fused"]
+    assert torch.equal(two[:, :, 1:], one[:, :, 1:]), "dk/dv differ"
+    a, b = two[:, :, 0].float(), one[:, :, 0].float()
+    assert ((a - b).norm() / a.norm()).item() <= DQ_VS_TWO_KERNEL
+    qf, kf, vf = (t.reshape(B, T, H, D).cpu() for t in fused.split((H * D, H * D, H * D), dim=-1))
+    rdq, _, _ = oracle.backward(qf, kf, vf, torch.ones(B, T, H, D), 70)
+    assert_grad("dq", b.cpu(), rdq)
