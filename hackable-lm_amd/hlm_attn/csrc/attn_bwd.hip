@@ -114,20 +114,14 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   const unsigned lring = lds_addr(ring);
   const unsigned stg_q = lring + PRE * SLOTB + wave * WSTG, stg_do = stg_q + NCH * 1024;
 
-  // 1. The wave's O rows (coalesced: chunk k = rows qw0 + RPC k + l / U) and lse.
-  bf16x8 oc[NCH];
-#pragma unroll
-  for (int k = 0; k < NCH; ++k)
-    oc[k] = buf_load_b128(ro, (qw0 + L::dma_row(k, lane)) * so2 + (lane % L::U) * 16);
-  float lraw = buf_load_b32(rl, myq * 4);  // 0 for rows >= T
-  // 2. Its Q and dO rows into the staging area (cs layout).
+  // 1. Its Q and dO rows into the staging area (cs layout).
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const int row = qw0 + L::dma_row(k, lane), cb = L::dma_col_bytes(k, lane);
     lds_dma_at<16>(rq, stg_q + k * 1024, row * sq2 + cb);
     lds_dma_at<16>(rdo, stg_do + k * 1024, row * sdo2 + cb);
   }
-  // 3. The first ring tiles.
+  // 2. The first ring tiles.
   const int key_lo = max(0, q0 - W + 1);
   const int key_hi = min(T, q0 + BM) - 1;
   const int t_lo = key_lo / BN, n_tiles = key_hi / BN - t_lo + 1;
@@ -160,7 +154,21 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
   const int n_pre = min(PRE, n_tiles);
   for (int t = 0; t < n_pre; ++t) load_tile(t);
 
-  // 4. Wait for this wave's rows (the first tiles may still be in flight).
+  // 3. The wave's O rows (coalesced: chunk k = rows qw0 + RPC k + l / U) and
+  // lse, into registers.  Issued after every copy: the compiler waits for
+  // these loads with counts that assume no other memory operation is in
+  // flight, so issued first, its wait for one of them (it once read the lse
+  // register as the unused half of a 64-bit address add) drained all copies
+  // issued after them.  Issued last, every wait for them also covers the
+  // copies, which the loop needs first anyway.
+  bf16x8 oc[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+    oc[k] = buf_load_b128(ro, (qw0 + L::dma_row(k, lane)) * so2 + (lane % L::U) * 16);
+  float lraw = buf_load_b32(rl, myq * 4);  // 0 for rows >= T
+
+  // 4. Wait for this wave's rows (the first tiles and the O rows may still be
+  // in flight: they are newer).
   vm_wait_upto<PER, PRE>(n_pre);
 
   int off_s[NS];
