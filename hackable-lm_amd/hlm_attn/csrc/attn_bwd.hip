@@ -572,6 +572,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(BwdArgs a) {
     kreg[s] = scale_bf16x8(kraw[s], c);
     vreg[s] = vraw[s];
   }
+  if constexpr (!STAGE_KV) {
+    // V's registers come straight from ordinary loads and are first read by
+    // the loop's dP products.  The compiler's wait for such loads counts only
+    // its own loads, so left to itself it puts a vmcnt(0) before that first
+    // read inside the loop, which then drains every tile copy in flight on
+    // every tile.  Reading them here puts that one wait in the prologue (it
+    // also covers the first tiles, which the loop needs next).
+#pragma unroll
+    for (int s = 0; s < NS; ++s) asm volatile("" : "+v"(vreg[s]));
+  }
 
   f32x16 dkacc[NDB], dvacc[NDB];
 #pragma unroll
