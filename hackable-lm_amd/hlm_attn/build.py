@@ -19,7 +19,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libhlm_attn.so"
-SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_bwd_fused.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
+SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_bwd_dkdv.hip", "attn_bwd_fused.hip", "qk_norm_rope.hip", "linear_ce.hip", "residual_norm.hip", "capi.hip")
 ARCH = "gfx950"
 PYCALL_PATH = PKG_DIR / ("_pycall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 TORCH_FWD_PATH = PKG_DIR / "_torch_fwd.so"
@@ -37,8 +37,10 @@ HIPCC_FLAGS = [
 ]
 # The attention kernels are scheduled with LLVM's iterative ILP strategy: on
 # the MI355X it took 1-5% off the forward and the dQ kernel across the
-# benchmark configs (bit-identical results); the bandwidth-bound kernels keep
-# the default scheduler.
+# benchmark configs (bit-identical results).  The dK/dV kernel keeps the
+# default scheduler, which honours its pipelined operand reads within three
+# waves per SIMD (iterative ILP spills there); so do the bandwidth-bound
+# kernels.
 PER_SOURCE_FLAGS = {
     "attn_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "attn_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],

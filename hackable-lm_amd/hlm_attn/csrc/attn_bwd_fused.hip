@@ -41,14 +41,6 @@ namespace hlm {
 
 namespace {
 
-// bf16 round of x * f, elementwise (as attn_bwd.hip forms its scaled K).
-__device__ __forceinline__ bf16x8 scale_bf16x8_f(bf16x8 x, float f) {
-  bf16x8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (bf16)((float)x[e] * f);
-  return r;
-}
-
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -248,7 +240,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_fused_kernel(BwdArgs a, 
   bf16x8 kreg[NS], vreg[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    kreg[s] = scale_bf16x8_f(cs_operand<D>(stg_k, off_s[s], 0), c);
+    kreg[s] = scale_bf16x8(cs_operand<D>(stg_k, off_s[s], 0), c);
     vreg[s] = cs_operand<D>(stg_v, off_s[s], 0);
   }
   // K^T (unscaled) as the A operand of this wave's dQ^T quarter, columns

@@ -125,6 +125,15 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// bf16 round of x * f, elementwise (the backward's operands pre-multiplied by
+// scale * log2(e)).
+__device__ __forceinline__ bf16x8 scale_bf16x8(bf16x8 x, float f) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)((float)x[e] * f);
+  return r;
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
