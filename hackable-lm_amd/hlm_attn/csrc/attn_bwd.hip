@@ -283,15 +283,23 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
         pacc = mfma32(vop[s], doreg[s], pacc);
       }
       bf16x8 dsb[2];
+      // dQ's K^T operands are read right after the S and dP products issue
+      // (into the registers their operands free), so the LDS latency hides
+      // under the softmax; placed by the compiler, half of them were read
+      // after it and waited for just before their products.
+      bf16x8 ktr[2][NDB];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          ktr[kk][db] = cs_operand_tr<D>(kt, cs_tr_off_from<D>((int)tb, db, 0), cs_tr_off_from<D>((int)tb, db, 1), 16 * kk);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          dqacc[db] = mfma32(cs_operand_tr<D>(kt, cs_tr_off_from<D>((int)tb, db, 0), cs_tr_off_from<D>((int)tb, db, 1),
-                                              16 * kk),
-                             dsb[kk], dqacc[db]);
+        for (int db = 0; db < NDB; ++db) dqacc[db] = mfma32(ktr[kk][db], dsb[kk], dqacc[db]);
     }
   } else {
     // D = 128 (one tile per group): the loop unrolled by the ring depth, so
