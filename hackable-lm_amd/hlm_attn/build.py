@@ -44,7 +44,6 @@ HIPCC_FLAGS = [
 PER_SOURCE_FLAGS = {
     "attn_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "attn_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
-    "attn_bwd_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
 

@@ -31,6 +31,9 @@
 // among them, and every slot the reduce reads for a row was written by the
 // workgroup of that key tile during the same call.
 //
+// Compiled with LLVM's default scheduler, which honours the pipelined S/dP
+// operand reads (as attn_bwd_dkdv.hip).
+//
 // Stores inside the tile loop count in vmcnt next to the ring's DMA loads.
 // Loads return in issue order, so a wait for "at most N outstanding" still
 // guarantees that all but the newest N loads are done; outstanding stores
@@ -403,11 +406,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_fused_kernel(BwdArgs a, 
         }
       }
       f32x16 sacc = si, pacc = di;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         sacc = mfma32(cs_operand<D>(qs_t, (int)ab_s[s], 0), kreg[s], sacc);
         pacc = mfma32(cs_operand<D>(ds_t, (int)ab_s[s], 0), vreg[s], pacc);
       }
+      // The row-operand reads run two ahead of their products, as in the
+      // dkdv kernel (attn_bwd_dkdv.hip).
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * NS - 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_barrier(0);
       bf16x8 pb[2];
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
