@@ -351,19 +351,26 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void attn_bwd_dq_kernel(BwdAr
           sacc[x] = (unsigned)(d0 - cst) < (unsigned)W ? sacc[x] : -INFINITY;
         }
       }
+      // As in the D = 128 forward, the wave raises its priority while it
+      // issues its products (two waves per SIMD; 1% faster at windows of
+      // 1024 and 2048 keys).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         sacc = mfma32(cs_operand<D>(kt, (int)ab_s[s], 0), qreg[s], sacc);
         pacc = mfma32(cs_operand<D>(vt, (int)ab_s[s], 0), doreg[s], pacc);
       }
+      __builtin_amdgcn_s_setprio(0);
       bf16x8 dsb[2];
 #pragma unroll
       for (int x = 0; x < 16; ++x) dsb[x >> 3][x & 7] = (bf16)(fast_exp2(sacc[x]) * pacc[x]);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
           dqacc[db] = mfma32(cs_operand_tr<D>(kt, (int)atr[db][0], (int)atr[db][1], 16 * kk), dsb[kk], dqacc[db]);
+      __builtin_amdgcn_s_setprio(0);
     }
   }
 

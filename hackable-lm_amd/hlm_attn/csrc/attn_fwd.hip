@@ -213,6 +213,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
     if (!(wave_live && k0 <= wq_hi && k0 + BN - 1 >= qw0 - W + 1)) continue;
     const bool full = (k0 + BN - 1 <= qw0) && (k0 >= qw0 + 32 - W);
 
+    // D = 128 (two waves per SIMD): the wave raises its priority while it
+    // issues its products, so the S and P V products of one wave are not held
+    // back behind the other wave's softmax instructions (1-2% faster at
+    // windows of 1024 and 2048 keys; no change at D = 64, three waves per
+    // SIMD).
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
     f32x16 sacc[BN / 32];
 #pragma unroll
     for (int kb = 0; kb < BN / 32; ++kb) {
@@ -233,6 +239,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
         }
     }
 
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
     bf16x8 pb[BN / 16];
     auto exponentiate = [&](const float mref) __attribute__((always_inline)) {
       float tsum = 0.f;
@@ -271,11 +278,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a) {
       tsum = exponentiate(mref);
     }
     lsum += tsum;
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int kk = 0; kk < BN / 16; ++kk)
         oacc[db] = mfma32(cs_operand_tr<D>(vt, (int)atr[db][0], (int)atr[db][1], 16 * kk), pb[kk], oacc[db]);
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
   }
 
   if constexpr (SPLIT) {
