@@ -552,6 +552,22 @@ def test_flop_model_matches_bench():
     assert math.isclose(bench.PEAK_BF16_TFLOPS, 256 * 4096 * 2.4e9 / 1e12, rel_tol=1e-4)
 
 
+@pytest.mark.parametrize("argv,env", [(["--gpus", "2"], {}), (["--gpus", "8"], {}), ([], {"WORLD_SIZE": "2"})])
+def test_bench_refuses_more_than_one_gpu(argv, env):
+    """`bench.py --gpus N` (or a launcher's WORLD_SIZE) with N > 1 exits with a
+    message before touching a device: this build measures one GPU."""
+    import os
+    import subprocess
+    import sys
+
+    root = Path(__file__).resolve().parent.parent
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), *argv], capture_output=True, text=True,
+                          env={**os.environ, **env}, timeout=120, cwd=root)
+    assert proc.returncode == 2
+    assert "measures one GPU" in proc.stderr
+    assert proc.stdout == ""
+
+
 def test_bench_config_synthesis():
     """cfg5's inputs: bench's fp32 RoPE equals the oracle's rotate-half
     restatement (model.py:105-114 at base 10000, fraction 1.0) on the same
